@@ -1,0 +1,192 @@
+/*
+ * pagedkv.h — C ABI of the MI355X (gfx950) paged-KV library.
+ *
+ * Plain pointers, sizes and a HIP stream handle (hipStream_t passed as void*;
+ * NULL means the null stream). Every device pointer is an ordinary device
+ * allocation (or pinned host memory where stated). No torch types cross this
+ * boundary. Every call is asynchronous on `stream` unless stated otherwise;
+ * the kernels never read or write out of bounds: an out-of-range page id or
+ * slot is skipped and reported through `status_word` (a device int32 whose
+ * bits are OR-ed in; see PKV_STATUS_*), which the caller reads at a declared
+ * check point.
+ *
+ * Return value: PKV_OK, or an error code with a message in pkv_last_error()
+ * (thread-local, valid until the next call on the same thread).
+ *
+ * Pool layout (the reference's, serving/backends/paged_torch.py:127-137):
+ * one allocation of `n_layers * 2` planes, plane (layer, kv) at
+ * base + (layer * 2 + kv) * plane_bytes, each plane a contiguous
+ * [num_blocks, page_size, n_kv_heads, head_dim] array. A per-layer K (or V)
+ * pool is exactly one plane, so a caller that only has per-layer tensors
+ * passes that plane's address to the per-layer entry points.
+ */
+#ifndef PAGEDKV_H
+#define PAGEDKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of the pool, q, k, v and out */
+#define PKV_DTYPE_F16 0
+#define PKV_DTYPE_BF16 1
+#define PKV_DTYPE_F32 2
+
+/* return codes */
+#define PKV_OK 0
+#define PKV_ERR_INVALID 1     /* argument or metadata error (Python: ValueError) */
+#define PKV_ERR_RANGE 2       /* block id out of range (Python: IndexError) */
+#define PKV_ERR_HIP 3         /* HIP runtime error */
+#define PKV_ERR_CAPACITY 4    /* caller-provided buffer too small */
+
+/* bits OR-ed into *status_word by the kernels */
+#define PKV_STATUS_BAD_SLOT 1   /* slot_mapping entry outside [0, num_slots) */
+#define PKV_STATUS_BAD_PAGE 2   /* kv_indices entry outside [0, num_blocks) */
+#define PKV_STATUS_BAD_BLOCK 4  /* copy/gather/scatter id outside [0, num_blocks) */
+
+/* Version of this ABI; bumped on any signature change. */
+int pkv_abi_version(void);
+
+/* Message for the last non-zero return on this thread ("" if none). */
+const char* pkv_last_error(void);
+
+/*
+ * KV append — replaces PagedTorchBackend.append_kv
+ * (serving/backends/paged_torch.py:209-276) and FlashInfer's
+ * append_paged_kv_cache call (serving/backends/flashinfer_backend.py:502-512):
+ * for t < n_tokens, row slot_mapping[t] of the flat [num_slots, n_kv_heads,
+ * head_dim] view of k_pool / v_pool receives row t of k / v. k and v are
+ * contiguous [n_tokens, n_kv_heads, head_dim] in the pool dtype.
+ * Idempotent. Slots outside [0, num_slots) are skipped and flagged.
+ */
+int pkv_append_kv(void* k_pool, void* v_pool, int64_t num_slots,
+                  const void* k, const void* v, const int32_t* slot_mapping,
+                  int64_t n_tokens, int32_t n_kv_heads, int32_t head_dim,
+                  int32_t dtype, int32_t* status_word, void* stream);
+
+/*
+ * Decode plan (host function, synchronous, no device access) — the
+ * counterpart of the reference fast path's plan step
+ * (serving/backends/flashinfer_backend.py:566-676), computed once per batch
+ * and reused by every layer. Splits each sequence's pages into partitions of
+ * at most `part_pages` pages (split-K over the KV axis; the split depends
+ * only on that sequence's own length) and orders the partitions longest
+ * first. Checks that every sequence has ceil(kv_len / page_size) pages and
+ * that kv_last_page_len agrees (PKV_ERR_INVALID, message naming
+ * kv_last_page_len, as serving/backends/paged_torch.py:379-392 does).
+ *
+ * Output `plan` (int32), capacity `plan_capacity` entries:
+ *   [0 .. 4*n_work)            work items {seq, first_page, n_pages, slot}
+ *                              (slot = -1: the item covers the whole sequence)
+ *   [4*n_work .. +3*n_merge)   merge items {seq, first_slot, n_slots}
+ * *n_slots_out is the number of partial-result slots the workspace must hold.
+ */
+int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_lens,
+                    const int32_t* kv_last_page_len, int32_t n_seqs,
+                    int32_t page_size, int32_t part_pages,
+                    int32_t* plan, int64_t plan_capacity,
+                    int32_t* n_work_out, int32_t* n_merge_out,
+                    int32_t* n_slots_out);
+
+/* Bytes of workspace pkv_attend_decode needs for `n_slots` partial slots. */
+int64_t pkv_decode_workspace_bytes(int32_t n_slots, int32_t n_heads, int32_t head_dim);
+
+/*
+ * Paged decode attention — replaces PagedTorchBackend.attend
+ * (serving/backends/paged_torch.py:280-485) and FlashInfer's decode wrapper
+ * run (serving/backends/flashinfer_backend.py:556-562, planned at :658-670)
+ * for batches where every sequence contributes exactly one query token
+ * (token i belongs to sequence i). q, out: [n_seqs, n_heads, head_dim];
+ * query head h reads KV head h / (n_heads / n_kv_heads); no mask (the
+ * single query is the last position). `plan` is the device copy of
+ * pkv_plan_decode's output; `workspace` holds the split-K partials.
+ */
+int pkv_attend_decode(const void* q, void* out,
+                      const void* k_pool, const void* v_pool, int64_t num_blocks,
+                      const int32_t* kv_indptr, const int32_t* kv_indices,
+                      const int32_t* kv_lens, int32_t n_seqs,
+                      int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                      int32_t page_size, float scale, int32_t dtype,
+                      const int32_t* plan, int32_t n_work, int32_t n_merge,
+                      int32_t n_slots, int32_t part_pages,
+                      void* workspace, int64_t workspace_bytes,
+                      int32_t* status_word, void* stream);
+
+/*
+ * Prefill plan (host function) — tiles each sequence's query rows for
+ * pkv_attend_prefill. Output `plan` = n_tiles items {seq, q_start, q_len,
+ * 0}, ordered by descending work.
+ */
+int pkv_plan_prefill(const int32_t* cu_query_lens, const int32_t* kv_indptr,
+                     const int32_t* kv_lens, const int32_t* kv_last_page_len,
+                     int32_t n_seqs, int32_t page_size, int32_t q_tile,
+                     int32_t* plan, int64_t plan_capacity, int32_t* n_tiles_out);
+
+/*
+ * Paged attention for arbitrary per-sequence query lengths (chunked prefill,
+ * mixed prefill+decode) — replaces PagedTorchBackend.attend
+ * (serving/backends/paged_torch.py:280-485) and FlashInfer's prefill wrapper
+ * run (serving/backends/flashinfer_backend.py:556-562, planned with
+ * causal=True at :635-649). Query j of sequence i (q_len_i queries,
+ * kv_len_i keys) attends keys [0, kv_len_i - q_len_i + j] (bottom-right
+ * causal). q, out: [n_tokens, n_heads, head_dim]. `batch_indices` maps each
+ * token to its sequence. `plan` is the device copy of pkv_plan_prefill's
+ * output (q_tile must match the one given to the plan).
+ */
+int pkv_attend_prefill(const void* q, void* out,
+                       const void* k_pool, const void* v_pool, int64_t num_blocks,
+                       const int32_t* cu_query_lens, const int32_t* kv_indptr,
+                       const int32_t* kv_indices, const int32_t* kv_lens,
+                       const int32_t* batch_indices,
+                       int32_t n_seqs, int32_t n_tokens,
+                       int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                       int32_t page_size, float scale, int32_t dtype,
+                       const int32_t* plan, int32_t n_tiles, int32_t q_tile,
+                       int32_t* status_word, void* stream);
+
+/*
+ * Batched block copy over every layer, K and V — replaces
+ * PagedTorchBackend.copy_block (serving/backends/paged_torch.py:181-207),
+ * called once per pair by RadixCache.ensure_writable
+ * (serving/cache/radix.py:672-674). For each pair p, block dst[p] of every
+ * plane becomes a copy of block src[p]. All sources are read before any
+ * destination is written only if no dst appears among the srcs; the caller
+ * guarantees that (and that dsts are distinct). Ids outside
+ * [0, num_blocks) are skipped and flagged.
+ */
+int pkv_copy_blocks(void* pool_base, int32_t n_layers, int64_t plane_bytes,
+                    int64_t block_bytes, int64_t num_blocks,
+                    const int32_t* src, const int32_t* dst, int32_t n_pairs,
+                    int32_t* status_word, void* stream);
+
+/*
+ * Swap-out gather — the device half of KVSwapSpace._to_host
+ * (serving/scheduler/preemption.py:490-509): staging[kv][layer][i] = block
+ * ids[i] of plane (layer, kv), i.e. staging is [2][n_layers][n_ids][block]
+ * (K half first), the reference's SwapHandle.k / .v layout
+ * (serving/scheduler/preemption.py:303-332). `staging` may be device memory
+ * or pinned host memory mapped for the device.
+ */
+int pkv_gather_blocks(const void* pool_base, int32_t n_layers, int64_t plane_bytes,
+                      int64_t block_bytes, int64_t num_blocks,
+                      const int32_t* ids, int32_t n_ids, void* staging,
+                      int32_t* status_word, void* stream);
+
+/*
+ * Swap-in scatter — the device half of KVSwapSpace._from_host
+ * (serving/scheduler/preemption.py:511-523): the inverse of
+ * pkv_gather_blocks; block ids[i] of plane (layer, kv) receives
+ * staging[kv][layer][i]. ids must be distinct.
+ */
+int pkv_scatter_blocks(void* pool_base, int32_t n_layers, int64_t plane_bytes,
+                       int64_t block_bytes, int64_t num_blocks,
+                       const int32_t* ids, int32_t n_ids, const void* staging,
+                       int32_t* status_word, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEDKV_H */

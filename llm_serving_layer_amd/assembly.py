@@ -1,0 +1,146 @@
+"""
+Scheduler state -> ``BatchMeta``.
+
+Follows serving/engine_iface/batch.py:77-318 in behaviour: each sequence's
+block table must already be grown to include this step's tokens, positions
+are absolute (``kv_len - q .. kv_len - 1``), the CSR triple comes from
+``build_csr``, and the same rejections with the same message fragments
+(``has been freed``, ``contributes 0 tokens``, ``blocks.append``,
+``page_size``).
+
+Different from the reference in one respect that matters on MI355X: all ten
+index arrays are packed into ONE pinned host buffer and uploaded with ONE
+non-blocking copy, then exposed as views. Ten separate ``torch.tensor(...,
+device=...)`` calls are ten synchronous H2D round trips per step.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from .contract import BatchMeta
+from .paging import SequenceBlocks, build_csr
+
+__all__ = ["ScheduledSeq", "build_batch_meta", "build_token_tensor"]
+
+
+@dataclass
+class ScheduledSeq:
+    """One sequence's contribution to one step; ``blocks`` is already grown."""
+
+    blocks: SequenceBlocks
+    new_token_ids: list[int] = field(default_factory=list)
+    wants_logits: bool = True
+
+    @property
+    def query_len(self) -> int:
+        return len(self.new_token_ids)
+
+    @property
+    def kv_len(self) -> int:
+        return self.blocks.num_tokens
+
+    @property
+    def start_position(self) -> int:
+        return self.kv_len - self.query_len
+
+    def positions(self) -> list[int]:
+        return list(range(self.start_position, self.kv_len))
+
+
+def _check_seq(i: int, s: ScheduledSeq) -> None:
+    sid = s.blocks.seq_id
+    if s.blocks.is_freed:
+        raise ValueError(f"seq {i} (seq_id={sid}) has been freed; its pages may belong "
+                         "to another sequence")
+    q, k = s.query_len, s.kv_len
+    if q <= 0:
+        raise ValueError(f"seq {i} (seq_id={sid}) contributes {q} tokens; a sequence "
+                         "with nothing to run must not be in the batch")
+    if q > k:
+        raise ValueError(f"seq {i} (seq_id={sid}) contributes {q} tokens but its block "
+                         f"table holds only {k}: blocks.append() must run before assembly")
+    if k > s.blocks.capacity:
+        raise ValueError(f"seq {i} (seq_id={sid}) claims kv_len={k} but its "
+                         f"{s.blocks.num_blocks} blocks hold {s.blocks.capacity} tokens")
+
+
+def build_token_tensor(seqs: list[ScheduledSeq], device) -> torch.Tensor:
+    flat: list[int] = []
+    for i, s in enumerate(seqs):
+        _check_seq(i, s)
+        flat.extend(s.new_token_ids)
+    return torch.tensor(flat, dtype=torch.int64, device=device)
+
+
+def build_batch_meta(seqs: list[ScheduledSeq], device, page_size: int,
+                     dtype_index: torch.dtype = torch.int32,
+                     validate: bool = True) -> BatchMeta:
+    if not seqs:
+        raise ValueError("build_batch_meta() called with an empty sequence list")
+    if page_size <= 0:
+        raise ValueError(f"page_size must be positive, got {page_size}")
+
+    n = len(seqs)
+    qlens = np.empty(n, dtype=np.int64)
+    kvlens = np.empty(n, dtype=np.int64)
+    for i, s in enumerate(seqs):
+        _check_seq(i, s)
+        if s.blocks.block_size != page_size:
+            raise ValueError(f"seq {i} (seq_id={s.blocks.seq_id}) has block_size="
+                             f"{s.blocks.block_size} but the batch declares "
+                             f"page_size={page_size}")
+        qlens[i] = s.query_len
+        kvlens[i] = s.kv_len
+
+    cu = np.zeros(n + 1, dtype=np.int64)
+    np.cumsum(qlens, out=cu[1:])
+    T = int(cu[-1])
+    positions = np.concatenate([np.arange(k - q, k) for q, k in zip(qlens, kvlens)])
+    batch_idx = np.repeat(np.arange(n), qlens)
+    slots = np.fromiter((sl for s in seqs for sl in s.blocks.slots_for_new_tokens(s.query_len)),
+                        dtype=np.int64, count=T)
+    indptr, indices, last = build_csr([s.blocks for s in seqs])
+
+    parts = {
+        "query_lens": qlens, "cu_query_lens": cu, "kv_lens": kvlens,
+        "last_token_ix": cu[1:] - 1, "kv_indptr": np.asarray(indptr, np.int64),
+        "kv_indices": np.asarray(indices, np.int64), "kv_last_page_len": np.asarray(last, np.int64),
+        "batch_indices": batch_idx, "slot_mapping": slots,
+    }
+    fields = _upload(parts, positions, device, dtype_index)
+    meta = BatchMeta(**fields, page_size=page_size, is_prefill=bool((qlens > 1).any()))
+    if validate:
+        meta.validate()
+    return meta
+
+
+def _upload(parts: dict, positions: np.ndarray, device, dtype_index: torch.dtype) -> dict:
+    """Pack every index array into one host buffer, move it once, slice views."""
+    device = torch.device(device)
+    idx_np = {torch.int32: np.int32, torch.int64: np.int64}[dtype_index]
+    names = list(parts)
+    sizes = [parts[k].shape[0] for k in names]
+    total = sum(sizes)
+    host = torch.empty(total, dtype=dtype_index,
+                       pin_memory=device.type == "cuda" and torch.cuda.is_available())
+    hv = host.numpy()
+    off = 0
+    for k, sz in zip(names, sizes):
+        hv[off:off + sz] = parts[k].astype(idx_np, copy=False)
+        off += sz
+    pos_host = torch.from_numpy(positions.astype(np.int64, copy=False))
+    if device.type == "cuda":
+        dev = host.to(device, non_blocking=True)
+        pos_dev = pos_host.to(device, non_blocking=True)
+    else:
+        dev, pos_dev = host, pos_host
+    out, off = {}, 0
+    for k, sz in zip(names, sizes):
+        out[k] = dev[off:off + sz]
+        off += sz
+    out["positions"] = pos_dev
+    return out

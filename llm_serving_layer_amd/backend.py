@@ -1,0 +1,383 @@
+"""
+MI355XBackend — a third implementation of the attention-backend contract,
+next to the reference's PagedTorchBackend (serving/backends/paged_torch.py)
+and FlashInferBackend (serving/backends/flashinfer_backend.py), running on
+hand-written gfx950 kernels through the C ABI in include/pagedkv.h.
+
+Drop-in surface (same as both reference backends):
+
+* constructor ``(num_layers, num_blocks, block_size, n_kv_heads, n_heads,
+  head_dim, device="cuda:0", dtype=torch.float16, *, ...)`` with the same
+  validation and messages (paged_torch.py:95-109), checked BEFORE the native
+  library is touched so errors do not depend on the machine
+  (flashinfer_backend.py:271-300);
+* ``k_pool[l]`` / ``v_pool[l]``: per-layer contiguous
+  ``[num_blocks, block_size, n_kv_heads, head_dim]`` tensors
+  (paged_torch.py:127-137). Here they are views of ONE allocation laid out
+  ``[num_layers, 2, num_blocks, block_size, n_kv_heads, head_dim]`` so that a
+  whole-block copy across every layer, or a swap, is one kernel launch;
+* ``append_kv`` / ``attend`` / ``copy_block`` and the accounting methods
+  (paged_torch.py:139-207), plus ``workspace_bytes()``, ``invalidate_plan()``
+  and the ``n_plans`` / ``n_runs`` counters (flashinfer_backend.py:354-394,
+  678-688);
+* plan once per ``BatchMeta`` identity and scale, run once per layer
+  (flashinfer_backend.py:566-676), including the ``is_prefill`` cross-check.
+
+Everything runs on torch's current stream of the backend's device. Not
+thread-safe and not re-entrant, like the reference backends.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import _native
+from .contract import BatchMeta
+
+__all__ = ["MI355XBackend", "is_available", "unavailable_reason"]
+
+_DTYPES = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16,
+           torch.float32: _native.DTYPE_F32}
+
+DEFAULT_PART_PAGES = 4   # split-K partition: 4 pages = 64 tokens per wave
+DEFAULT_Q_TILE = 64
+
+
+def is_available() -> bool:
+    """True if the gfx950 library loads in this process (says nothing of a GPU)."""
+    return _native.available()
+
+
+def unavailable_reason() -> str | None:
+    return _native.reason()
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+class _Plan:
+    """Device-side metadata and launch plan for one BatchMeta (one step)."""
+
+    __slots__ = ("meta", "scale", "use_prefill", "slots", "indptr", "indices", "kv_lens",
+                 "cu_q", "bidx", "plan", "n_work", "n_merge", "n_slots", "n_tokens",
+                 "n_seqs")
+
+
+class MI355XBackend:
+    """Paged KV storage plus attention on gfx950 kernels."""
+
+    def __init__(self, num_layers: int, num_blocks: int, block_size: int, n_kv_heads: int,
+                 n_heads: int, head_dim: int, device: str | torch.device = "cuda:0",
+                 dtype: torch.dtype = torch.float16, *,
+                 part_pages: int = DEFAULT_PART_PAGES, q_tile: int = DEFAULT_Q_TILE):
+        if n_heads % n_kv_heads != 0:
+            raise ValueError(
+                f"n_heads={n_heads} must be divisible by n_kv_heads={n_kv_heads}; "
+                "GQA maps query head h to KV head h // (n_heads // n_kv_heads)."
+            )
+        for name, val in (("num_layers", num_layers), ("num_blocks", num_blocks),
+                          ("block_size", block_size), ("n_kv_heads", n_kv_heads),
+                          ("n_heads", n_heads), ("head_dim", head_dim)):
+            if val <= 0:
+                raise ValueError(f"{name} must be positive, got {val}")
+        if dtype not in _DTYPES:
+            raise ValueError(f"MI355XBackend supports float16, bfloat16 and float32 pools, "
+                             f"got {dtype}")
+        if head_dim > 256:
+            raise ValueError(f"head_dim={head_dim} > 256 is not supported")
+        try:
+            self._lib = _native.load()
+        except RuntimeError as exc:
+            raise RuntimeError(
+                f"MI355XBackend requires the gfx950 paged-KV library: {exc}\n"
+                "Use PagedTorchBackend (the correctness oracle) instead, or build the "
+                "library. Check availability without raising via "
+                "llm_serving_layer_amd.backend.is_available()."
+            ) from exc
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError(f"MI355XBackend requires a GPU device, got {self.device}. "
+                             "PagedTorchBackend is the CPU path.")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+
+        self.num_layers, self.num_blocks, self.block_size = num_layers, num_blocks, block_size
+        self.n_kv_heads, self.n_heads, self.head_dim = n_kv_heads, n_heads, head_dim
+        self.dtype = dtype
+        self.groups = n_heads // n_kv_heads
+        self.part_pages = part_pages
+        self.q_tile = q_tile
+        self._code = _DTYPES[dtype]
+
+        self._pool = torch.zeros((num_layers, 2, num_blocks, block_size, n_kv_heads, head_dim),
+                                 dtype=dtype, device=self.device)
+        self.k_pool: list[torch.Tensor] = [self._pool[l, 0] for l in range(num_layers)]
+        self.v_pool: list[torch.Tensor] = [self._pool[l, 1] for l in range(num_layers)]
+        self._block_bytes = block_size * n_kv_heads * head_dim * self._pool.element_size()
+        self._plane_bytes = num_blocks * self._block_bytes
+        self._status = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._workspace = torch.empty(0, dtype=torch.uint8, device=self.device)
+        self._planned: _Plan | None = None
+        self._slot_cache: tuple[BatchMeta, torch.Tensor] | None = None
+        self.n_plans = 0
+        self.n_runs = 0
+
+    # -- pool construction / accounting ---------------------------------------
+
+    def zeros_like_pool(self) -> torch.Tensor:
+        return torch.zeros_like(self.k_pool[0])
+
+    def pool_bytes(self) -> int:
+        return self.num_layers * 2 * self._plane_bytes
+
+    def block_bytes(self) -> int:
+        return self.pool_bytes() // self.num_blocks
+
+    def workspace_bytes(self) -> int:
+        """Split-K partials; grows with the largest batch planned, not with the pool."""
+        return self._workspace.numel()
+
+    def tokens_capacity(self) -> int:
+        return self.num_blocks * self.block_size
+
+    @staticmethod
+    def estimate_pool_bytes(num_layers: int, num_blocks: int, block_size: int,
+                            n_kv_heads: int, head_dim: int,
+                            dtype: torch.dtype = torch.float16) -> int:
+        elem = torch.empty((), dtype=dtype).element_size()
+        return num_layers * 2 * num_blocks * block_size * n_kv_heads * head_dim * elem
+
+    # -- helpers -----------------------------------------------------------------
+
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _check_layer(self, layer_idx) -> None:
+        if layer_idx is None or not 0 <= layer_idx < self.num_layers:
+            raise ValueError(f"layer_idx {layer_idx} out of range [0, {self.num_layers})")
+
+    def _dev_i32(self, t: torch.Tensor) -> torch.Tensor:
+        return t.to(device=self.device, dtype=torch.int32).contiguous()
+
+    def _as_pool(self, x: torch.Tensor) -> torch.Tensor:
+        return x.to(device=self.device, dtype=self.dtype).contiguous()
+
+    def check_device_errors(self) -> None:
+        """
+        Declared check point: synchronise and raise if any kernel since the
+        last check skipped an out-of-range slot, page or block id.
+        """
+        bits = int(self._status.item())
+        if bits:
+            self._status.zero_()
+            what = []
+            if bits & _native.STATUS_BAD_SLOT:
+                what.append("slot_mapping entry outside the pool")
+            if bits & _native.STATUS_BAD_PAGE:
+                what.append("kv_indices entry outside [0, num_blocks)")
+            if bits & _native.STATUS_BAD_BLOCK:
+                what.append("block id outside [0, num_blocks)")
+            raise IndexError("device kernels skipped invalid ids: " + "; ".join(what))
+
+    # -- write path -----------------------------------------------------------------
+
+    def copy_block(self, src: int, dst: int) -> None:
+        """Duplicate one block's KV in every layer (copy-on-write)."""
+        if not (0 <= src < self.num_blocks and 0 <= dst < self.num_blocks):
+            raise IndexError(f"copy_block({src} -> {dst}) outside [0, {self.num_blocks})")
+        if src == dst:
+            return
+        self.copy_blocks([src], [dst])
+
+    def copy_blocks(self, src, dst) -> None:
+        """
+        Batched ``copy_block``: one launch for every (src, dst) pair, every
+        layer, K and V. Destinations must be distinct and must not appear among
+        the sources (so the result cannot depend on the order of the pairs).
+        """
+        src = [int(s) for s in src]
+        dst = [int(d) for d in dst]
+        if len(src) != len(dst):
+            raise ValueError(f"{len(src)} sources but {len(dst)} destinations")
+        for s, d in zip(src, dst):
+            if not (0 <= s < self.num_blocks and 0 <= d < self.num_blocks):
+                raise IndexError(f"copy_block({s} -> {d}) outside [0, {self.num_blocks})")
+        pairs = [(s, d) for s, d in zip(src, dst) if s != d]
+        if not pairs:
+            return
+        ds = [d for _, d in pairs]
+        if len(set(ds)) != len(ds) or set(ds) & {s for s, _ in pairs}:
+            raise ValueError("copy_blocks needs distinct destinations that are not also sources")
+        ids = torch.tensor([s for s, _ in pairs] + ds, dtype=torch.int32).to(self.device)
+        n = len(pairs)
+        rc = self._lib.pkv_copy_blocks(self._pool.data_ptr(), self.num_layers,
+                                       self._plane_bytes, self._block_bytes, self.num_blocks,
+                                       ids.data_ptr(), ids.data_ptr() + 4 * n, n,
+                                       self._status.data_ptr(), self._stream())
+        _native.check(rc, "copy_blocks")
+
+    def append_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor,
+                  meta: BatchMeta) -> None:
+        """Scatter this step's K/V into the pool through ``meta.slot_mapping``."""
+        self._check_layer(layer_idx)
+        if meta.slot_mapping is None:
+            raise ValueError("MI355XBackend.append_kv requires meta.slot_mapping")
+        tokens = k.shape[0]
+        if tuple(k.shape) != (tokens, self.n_kv_heads, self.head_dim):
+            raise ValueError(f"k has shape {tuple(k.shape)}, expected "
+                             f"({tokens}, {self.n_kv_heads}, {self.head_dim})")
+        if v.shape != k.shape:
+            raise ValueError(f"v shape {tuple(v.shape)} != k shape {tuple(k.shape)}")
+        if meta.slot_mapping.shape[0] != tokens:
+            raise ValueError(f"slot_mapping has {meta.slot_mapping.shape[0]} entries but "
+                             f"{tokens} tokens were supplied")
+        sc = self._slot_cache
+        if sc is not None and sc[0] is meta:
+            slots = sc[1]
+        else:
+            slots = self._dev_i32(meta.slot_mapping)
+            self._slot_cache = (meta, slots)
+        k = self._as_pool(k)
+        v = self._as_pool(v)
+        rc = self._lib.pkv_append_kv(
+            self.k_pool[layer_idx].data_ptr(), self.v_pool[layer_idx].data_ptr(),
+            self.num_blocks * self.block_size, k.data_ptr(), v.data_ptr(), slots.data_ptr(),
+            tokens, self.n_kv_heads, self.head_dim, self._code, self._status.data_ptr(),
+            self._stream())
+        _native.check(rc, "append_kv")
+
+    # -- read path ------------------------------------------------------------------
+
+    def attend(self, q: torch.Tensor, layer_idx: int, scale: float,
+               meta: BatchMeta) -> torch.Tensor:
+        """Causal GQA attention over each sequence's full paged history."""
+        self._check_layer(layer_idx)
+        tokens = q.shape[0]
+        if tuple(q.shape) != (tokens, self.n_heads, self.head_dim):
+            raise ValueError(f"q has shape {tuple(q.shape)}, expected "
+                             f"({tokens}, {self.n_heads}, {self.head_dim})")
+        if meta.n_tokens != tokens:
+            raise ValueError(f"meta describes {meta.n_tokens} tokens but q has {tokens}")
+        p = self._ensure_planned(meta, scale)
+        q = self._as_pool(q)
+        out = torch.empty_like(q)
+        kp = self.k_pool[layer_idx].data_ptr()
+        vp = self.v_pool[layer_idx].data_ptr()
+        self.n_runs += 1
+        if not p.use_prefill:
+            ws = self._workspace
+            rc = self._lib.pkv_attend_decode(
+                q.data_ptr(), out.data_ptr(), kp, vp, self.num_blocks, p.indptr.data_ptr(),
+                p.indices.data_ptr(), p.kv_lens.data_ptr(), p.n_seqs, self.n_heads,
+                self.n_kv_heads, self.head_dim, self.block_size, float(scale), self._code,
+                p.plan.data_ptr(), p.n_work, p.n_merge, p.n_slots, self.part_pages,
+                ws.data_ptr() if ws.numel() else None, ws.numel(), self._status.data_ptr(),
+                self._stream())
+            _native.check(rc, "attend (decode)")
+        else:
+            rc = self._lib.pkv_attend_prefill(
+                q.data_ptr(), out.data_ptr(), kp, vp, self.num_blocks, p.cu_q.data_ptr(),
+                p.indptr.data_ptr(), p.indices.data_ptr(), p.kv_lens.data_ptr(),
+                p.bidx.data_ptr(), p.n_seqs, p.n_tokens, self.n_heads, self.n_kv_heads,
+                self.head_dim, self.block_size, float(scale), self._code, p.plan.data_ptr(),
+                p.n_work, self.q_tile, self._status.data_ptr(), self._stream())
+            _native.check(rc, "attend (prefill)")
+        return out
+
+    # -- planning ---------------------------------------------------------------
+
+    def _ensure_planned(self, meta: BatchMeta, scale: float) -> _Plan:
+        """
+        Build the launch plan for ``meta`` at most once per forward pass.
+        Keyed on the object identity of the (frozen) BatchMeta plus the scale,
+        with a strong reference held so the identity cannot be recycled.
+        """
+        pl = self._planned
+        if pl is not None and pl.meta is meta and pl.scale == scale:
+            return pl
+        n = meta.n_seqs
+        # ONE device->host transfer for everything the host plan reads.
+        host = torch.cat([meta.query_lens.reshape(-1).to(torch.int64),
+                          meta.cu_query_lens.reshape(-1).to(torch.int64),
+                          meta.kv_lens.reshape(-1).to(torch.int64),
+                          meta.kv_indptr.reshape(-1).to(torch.int64),
+                          meta.kv_last_page_len.reshape(-1).to(torch.int64)]).cpu().numpy()
+        ql, cu = host[:n], host[n:2 * n + 1]
+        kvl, indptr = host[2 * n + 1:3 * n + 1], host[3 * n + 1:4 * n + 2]
+        last = host[4 * n + 2:]
+        use_prefill = bool((ql > 1).any())
+        if bool(meta.is_prefill) != use_prefill:
+            raise ValueError(
+                f"BatchMeta.is_prefill={meta.is_prefill} disagrees with query_lens "
+                f"(max={int(ql.max())}). is_prefill must be True iff some sequence "
+                "contributes more than one token."
+            )
+        i32 = lambda a: np.ascontiguousarray(a, dtype=np.int32)  # noqa: E731
+        kvl32, indptr32, last32, cu32 = i32(kvl), i32(indptr), i32(last), i32(cu)
+        ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
+        p = _Plan()
+        p.meta, p.scale, p.use_prefill = meta, scale, use_prefill
+        p.n_seqs, p.n_tokens = n, int(cu[-1])
+        if p.n_tokens != meta.n_tokens:
+            raise ValueError(f"cu_query_lens ends at {p.n_tokens} but meta has "
+                             f"{meta.n_tokens} positions")
+        if int(indptr[0]) != 0 or int(indptr[-1]) != int(meta.kv_indices.shape[0]):
+            raise ValueError(f"kv_indptr spans [{int(indptr[0])}, {int(indptr[-1])}) but "
+                             f"kv_indices holds {int(meta.kv_indices.shape[0])} pages")
+        if int(meta.batch_indices.shape[0]) != p.n_tokens:
+            raise ValueError(f"batch_indices has {int(meta.batch_indices.shape[0])} entries "
+                             f"for {p.n_tokens} tokens")
+        n_work, n_merge, n_slots = C.c_int32(), C.c_int32(), C.c_int32()
+        if not use_prefill:
+            cap = 4 * (int(indptr[-1]) + n) + 3 * n
+            buf = np.empty(max(cap, 4), dtype=np.int32)
+            rc = self._lib.pkv_plan_decode(ptr(indptr32), ptr(kvl32), ptr(last32), n,
+                                           self.block_size, self.part_pages, ptr(buf), cap,
+                                           C.byref(n_work), C.byref(n_merge), C.byref(n_slots))
+            _native.check(rc, "plan (decode)")
+            used = 4 * n_work.value + 3 * n_merge.value
+            p.n_work, p.n_merge, p.n_slots = n_work.value, n_merge.value, n_slots.value
+            need = self._lib.pkv_decode_workspace_bytes(p.n_slots, self.n_heads, self.head_dim)
+            if need > self._workspace.numel():
+                self._workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
+        else:
+            cap = 4 * (int(cu[-1]) // self.q_tile + n + 1)
+            buf = np.empty(cap, dtype=np.int32)
+            rc = self._lib.pkv_plan_prefill(ptr(cu32), ptr(indptr32), ptr(kvl32), ptr(last32),
+                                            n, self.block_size, self.q_tile, ptr(buf), cap,
+                                            C.byref(n_work))
+            _native.check(rc, "plan (prefill)")
+            used = 4 * n_work.value
+            p.n_work, p.n_merge, p.n_slots = n_work.value, 0, 0
+        p.plan = torch.from_numpy(buf[:used].copy()).to(self.device)
+        p.indptr = self._dev_i32(meta.kv_indptr)
+        p.indices = self._dev_i32(meta.kv_indices)
+        p.kv_lens = self._dev_i32(meta.kv_lens)
+        p.cu_q = self._dev_i32(meta.cu_query_lens)
+        p.bidx = self._dev_i32(meta.batch_indices)
+        self._planned = p
+        self.n_plans += 1
+        return p
+
+    def invalidate_plan(self) -> None:
+        """Force the next ``attend`` to re-plan (and drop the cached meta)."""
+        self._planned = None
+        self._slot_cache = None
+
+    # -- misc -------------------------------------------------------------------------
+
+    def reset(self) -> None:
+        """Zero every pool and drop the plan. Tests only."""
+        self._pool.zero_()
+        self.invalidate_plan()
+
+    def __repr__(self) -> str:
+        mib = self.pool_bytes() / (1024 * 1024)
+        return (f"MI355XBackend(layers={self.num_layers}, blocks={self.num_blocks}, "
+                f"block_size={self.block_size}, kv_heads={self.n_kv_heads}, "
+                f"heads={self.n_heads}, head_dim={self.head_dim}, dtype={self.dtype}, "
+                f"device={self.device}, pool={mib:.1f} MiB)")

@@ -1,0 +1,172 @@
+"""
+The per-step batch description and the attention-backend protocol.
+
+The reference imports both types from its engine submodule
+(``engine.attention_backend``, imported at serving/backends/paged_torch.py:66
+and serving/engine_iface/batch.py:62), which is not vendored. They are
+restated here from their documented contract:
+
+* fields and dtypes: docs/ARCHITECTURE.md:92-117;
+* protocol and per-layer call order: docs/ARCHITECTURE.md:152-174;
+* ``validate()`` behaviour, including the message fragments callers match
+  (``kv_last_page_len``, ``pages allocated``, ``batch_indices``):
+  tests/test_batch_assembly.py:345-384;
+* ``n_seqs`` / ``n_tokens``: tests/test_batch_assembly.py:67-69,132.
+
+``BatchMeta`` is frozen: one object describes one forward pass and is passed,
+unchanged, to every layer's ``append_kv`` and ``attend``. Backends rely on
+that to cache a launch plan by object identity.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional, Protocol, runtime_checkable
+
+import torch
+
+__all__ = ["BatchMeta", "AttentionBackend"]
+
+
+def _host_list(t: torch.Tensor) -> list[int]:
+    return [int(x) for x in t.detach().to("cpu").reshape(-1).tolist()]
+
+
+@dataclass(frozen=True)
+class BatchMeta:
+    """
+    One forward pass over a ragged batch.
+
+    Tokens of all sequences are packed along axis 0 in sequence order;
+    sequence ``i`` owns ``[cu_query_lens[i], cu_query_lens[i + 1])``.
+
+    query_lens        (n,)    int32  new tokens of each sequence this step
+    cu_query_lens     (n+1,)  int32  exclusive prefix sum of query_lens
+    kv_lens           (n,)    int32  KV length AFTER this step's append
+    positions         (T,)    int64  absolute position of each new token
+    kv_indptr         (n+1,)  int32  CSR row pointer into kv_indices
+    kv_indices        (P,)    int32  physical page ids, sequence after sequence
+    kv_last_page_len  (n,)    int32  tokens on each sequence's last page, 1..page_size
+    batch_indices     (T,)    int32  owning sequence of each new token
+    slot_mapping      (T,)    int32  flat pool slot of each new token (or None)
+    last_token_ix     (n,)    int32  packed index of each sequence's last token
+    page_size         tokens per page
+    is_prefill        hint: True iff some sequence contributes > 1 token
+    """
+
+    query_lens: torch.Tensor
+    cu_query_lens: torch.Tensor
+    kv_lens: torch.Tensor
+    positions: torch.Tensor
+    kv_indptr: torch.Tensor
+    kv_indices: torch.Tensor
+    kv_last_page_len: torch.Tensor
+    batch_indices: torch.Tensor
+    slot_mapping: Optional[torch.Tensor]
+    last_token_ix: torch.Tensor
+    page_size: int = 16
+    is_prefill: bool = False
+
+    @property
+    def n_seqs(self) -> int:
+        return int(self.query_lens.shape[0])
+
+    @property
+    def n_tokens(self) -> int:
+        # Shape-derived on purpose: backends compare it once per layer and a
+        # value read (cu_query_lens[-1]) would cost a device sync each time.
+        return int(self.positions.shape[0])
+
+    def validate(self) -> None:
+        """
+        Assert every structural invariant whose violation would otherwise be
+        silent (wrong pages read, a page dropped, a token routed to another
+        sequence). Raises ``AssertionError``. Pulls the fields to the host
+        once; it is meant for batch assembly, not for the per-layer path.
+        """
+        n = self.n_seqs
+        ps = int(self.page_size)
+        assert ps > 0, f"page_size must be positive, got {ps}"
+        assert n > 0, "BatchMeta describes no sequences"
+
+        ql = _host_list(self.query_lens)
+        cu = _host_list(self.cu_query_lens)
+        kv = _host_list(self.kv_lens)
+        indptr = _host_list(self.kv_indptr)
+        last = _host_list(self.kv_last_page_len)
+        ltok = _host_list(self.last_token_ix)
+        pos = _host_list(self.positions)
+        bidx = _host_list(self.batch_indices)
+
+        for name, vals in (("kv_lens", kv), ("kv_last_page_len", last),
+                           ("last_token_ix", ltok)):
+            assert len(vals) == n, f"{name} has {len(vals)} entries for {n} sequences"
+        assert len(cu) == n + 1, f"cu_query_lens has {len(cu)} entries, expected {n + 1}"
+        assert len(indptr) == n + 1, f"kv_indptr has {len(indptr)} entries, expected {n + 1}"
+
+        assert cu[0] == 0, f"cu_query_lens must start at 0, got {cu[0]}"
+        for i in range(n):
+            assert cu[i + 1] - cu[i] == ql[i], (
+                f"cu_query_lens {cu[i]}..{cu[i + 1]} disagrees with query_lens[{i}]={ql[i]}"
+            )
+        tokens = cu[-1]
+        assert len(pos) == tokens, f"positions has {len(pos)} entries for {tokens} tokens"
+        assert len(bidx) == tokens, (
+            f"batch_indices has {len(bidx)} entries for {tokens} tokens"
+        )
+        if self.slot_mapping is not None:
+            ns = int(self.slot_mapping.shape[0])
+            assert ns == tokens, f"slot_mapping has {ns} entries for {tokens} tokens"
+
+        assert indptr[0] == 0, f"kv_indptr must start at 0, got {indptr[0]}"
+        n_pages_total = int(self.kv_indices.shape[0])
+        assert indptr[-1] == n_pages_total, (
+            f"kv_indptr ends at {indptr[-1]} but kv_indices holds {n_pages_total} pages"
+        )
+
+        for i in range(n):
+            assert 1 <= last[i] <= ps, (
+                f"seq {i}: kv_last_page_len={last[i]} outside [1, {ps}]; an exact "
+                f"multiple of page_size reports {ps}, never 0"
+            )
+            assert 1 <= ql[i] <= kv[i], (
+                f"seq {i}: query_len={ql[i]} must lie in [1, kv_len={kv[i]}]"
+            )
+            pages = indptr[i + 1] - indptr[i]
+            need = (kv[i] + ps - 1) // ps
+            assert pages == need, (
+                f"seq {i}: kv_len={kv[i]} needs {need} pages but {pages} pages allocated"
+            )
+            assert kv[i] - (pages - 1) * ps == last[i], (
+                f"seq {i}: kv_last_page_len={last[i]} but kv_len={kv[i]} over "
+                f"{pages} pages implies {kv[i] - (pages - 1) * ps}"
+            )
+            assert ltok[i] == cu[i + 1] - 1, (
+                f"seq {i}: last_token_ix={ltok[i]}, expected {cu[i + 1] - 1}"
+            )
+            for j in range(ql[i]):
+                t = cu[i] + j
+                assert bidx[t] == i, f"batch_indices[{t}]={bidx[t]}, expected {i}"
+                want = kv[i] - ql[i] + j
+                assert pos[t] == want, (
+                    f"positions[{t}]={pos[t]}, expected absolute position {want}"
+                )
+        # is_prefill is a hint, not an invariant: backends that dispatch on it
+        # cross-check it against query_lens themselves and raise ValueError.
+
+
+@runtime_checkable
+class AttentionBackend(Protocol):
+    """
+    What a model's forward pass calls, per layer, in this order
+    (docs/ARCHITECTURE.md:166-174): ``append_kv`` then ``attend``, so a
+    decoding token attends to the K/V it just wrote.
+    """
+
+    def append_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor,
+                  meta: BatchMeta) -> None:
+        """Write this step's ``(tokens, n_kv_heads, head_dim)`` K/V into the pool."""
+
+    def attend(self, q: torch.Tensor, layer_idx: int, scale: float,
+               meta: BatchMeta) -> torch.Tensor:
+        """Causal (bottom-right) GQA attention; returns a new tensor shaped like q."""

@@ -1,0 +1,12 @@
+"""
+ORACLE — test infrastructure. CPU restatements of the reference's paged-KV
+path used only as the checker by tests/, ``__graft_entry__.smoke()`` and the
+CPU-baseline leg of bench.py. Nothing in llm_serving_layer_amd/ imports it.
+"""
+
+from .naive import (append_closed_form, copy_blocks_closed_form, gather_closed_form,
+                    naive_attention, scatter_closed_form)
+from .paged_torch_cpu import PagedTorchOracle
+
+__all__ = ["PagedTorchOracle", "naive_attention", "append_closed_form",
+           "copy_blocks_closed_form", "gather_closed_form", "scatter_closed_form"]

@@ -1,0 +1,105 @@
+"""Shared test helpers: batch construction the way a scheduler does it."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from llm_serving_layer_amd import (BatchMeta, BlockAllocator, ScheduledSeq, SequenceBlocks,
+                                   build_batch_meta, build_csr)
+
+
+def make_meta(seqs: list[SequenceBlocks], query_lens: list[int], block_size: int,
+              device="cpu") -> BatchMeta:
+    """
+    Hand-assemble a BatchMeta from grown block tables, independently of
+    build_batch_meta (the reference's own tests do the same,
+    tests/test_paged_torch.py:66-103), then validate it.
+    """
+    indptr, indices, last = build_csr(seqs)
+    slots, positions, bidx = [], [], []
+    for i, (s, ql) in enumerate(zip(seqs, query_lens)):
+        slots.extend(s.slots_for_new_tokens(ql))
+        positions.extend(range(s.num_tokens - ql, s.num_tokens))
+        bidx.extend([i] * ql)
+    cu = [0]
+    for ql in query_lens:
+        cu.append(cu[-1] + ql)
+
+    def i32(x):
+        return torch.tensor(x, dtype=torch.int32, device=device)
+
+    meta = BatchMeta(
+        query_lens=i32(query_lens), cu_query_lens=i32(cu),
+        kv_lens=i32([s.num_tokens for s in seqs]),
+        positions=torch.tensor(positions, dtype=torch.int64, device=device),
+        kv_indptr=i32(indptr), kv_indices=i32(indices), kv_last_page_len=i32(last),
+        batch_indices=i32(bidx), slot_mapping=i32(slots),
+        last_token_ix=i32([cu[i + 1] - 1 for i in range(len(seqs))]),
+        page_size=block_size, is_prefill=any(q > 1 for q in query_lens),
+    )
+    meta.validate()
+    return meta
+
+
+def grow_and_assemble(blocks: list[SequenceBlocks], counts: list[int], block_size: int,
+                      device="cpu") -> BatchMeta:
+    """Grow each table by counts[i] (0 = not scheduled) and assemble for real."""
+    scheds = []
+    for b, n in zip(blocks, counts):
+        if n == 0:
+            continue
+        b.append(n)
+        scheds.append(ScheduledSeq(blocks=b, new_token_ids=[0] * n))
+    return build_batch_meta(scheds, device=device, page_size=block_size)
+
+
+def fragmented_allocator(num_blocks: int, block_size: int) -> tuple[BlockAllocator, list]:
+    """
+    Exhaust the pool, then free every other block: later allocations receive
+    scattered, non-monotonic ids (the FIFO free list only hands out holes).
+    """
+    alloc = BlockAllocator(num_blocks=num_blocks, block_size=block_size)
+    holders = [SequenceBlocks(alloc, seq_id=900 + i) for i in range(num_blocks)]
+    for h in holders:
+        h.append(block_size)
+    assert alloc.num_free == 0
+    for h in holders[::2]:
+        h.free()
+    return alloc, holders[1::2]
+
+
+def lognormal_lengths(n: int, mean_len: int, sigma: float, max_seq: int, seed: int) -> list[int]:
+    """The reference's length law (bench/capacity.py:196-242), lognormal branch."""
+    import math
+    import random
+
+    rng = random.Random(seed)
+    mu = math.log(mean_len) - sigma ** 2 / 2.0
+    return [max(1, min(max_seq, int(round(rng.lognormvariate(mu, sigma))))) for _ in range(n)]
+
+
+def assert_attention_close(got: torch.Tensor, want: torch.Tensor, atol=2e-3, rtol=1e-2,
+                           label=""):
+    """
+    Parity bar for attention outputs against the fp32 reference computation:
+    max |got - want| <= atol everywhere, and |got - want| / |want| <= rtol
+    wherever |want| > atol / rtol (below that the absolute bound is the
+    tighter one).
+    """
+    g = got.detach().float().cpu()
+    w = want.detach().float().cpu()
+    assert g.shape == w.shape, f"{label}: shape {tuple(g.shape)} != {tuple(w.shape)}"
+    assert torch.isfinite(g).all(), f"{label}: non-finite output"
+    d = (g - w).abs()
+    max_abs = float(d.max()) if d.numel() else 0.0
+    assert max_abs <= atol, f"{label}: max|delta|={max_abs:.3g} > atol {atol}"
+    big = w.abs() > atol / rtol
+    if bool(big.any()):
+        max_rel = float((d[big] / w.abs()[big]).max())
+        assert max_rel <= rtol, f"{label}: max relative error {max_rel:.3g} > rtol {rtol}"
+    return max_abs
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()

@@ -1,0 +1,325 @@
+"""
+GPU parity of paged attention against the oracle.
+
+Bar (the north star's): fp16/bf16 output within max-abs 2e-3 / max-rel 1e-2
+of the oracle's fp32 computation on the same (fp16-rounded) inputs; fp32
+pools within 1e-5 of the float64 textbook. Structural known answers from the
+reference's tests/test_paged_torch.py (:303-649) and the differential harness
+of tests/test_flashinfer_differential.py (:381-600: pure decode, mixed,
+page-boundary sweep, fragmented + poisoned pools, isolation, GQA 8->{1,2,4,8},
+plan once per step) are restated against this backend.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from llm_serving_layer_amd import BlockAllocator, SequenceBlocks
+from llm_serving_layer_amd.backend import MI355XBackend
+from oracle import PagedTorchOracle
+
+from ._util import (assert_attention_close, fragmented_allocator, grow_and_assemble,
+                    lognormal_lengths, make_meta)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+class Pair:
+    """The GPU backend and the CPU fp32 oracle fed identical (dtype-rounded) inputs."""
+
+    def __init__(self, num_layers, num_blocks, block_size, n_kv, n_heads, head_dim,
+                 dtype=torch.float16, part_pages=4):
+        self.gpu = MI355XBackend(num_layers, num_blocks, block_size, n_kv, n_heads, head_dim,
+                                 device=DEV, dtype=dtype, part_pages=part_pages)
+        self.ref = PagedTorchOracle(num_layers, num_blocks, block_size, n_kv, n_heads, head_dim,
+                                    device="cpu", dtype=torch.float32)
+        self.dtype = dtype
+
+    def poison(self, seed):
+        g = torch.Generator().manual_seed(seed)
+        x = torch.randn(self.gpu._pool.shape, generator=g).to(self.dtype)
+        self.gpu._pool.copy_(x.to(DEV))
+        for l in range(self.gpu.num_layers):
+            self.ref.k_pool[l].copy_(x[l, 0].float())
+            self.ref.v_pool[l].copy_(x[l, 1].float())
+
+    def rand(self, shape, g, scale=1.0):
+        return (torch.randn(shape, generator=g) * scale).to(self.dtype)
+
+    def step(self, meta_cpu, seed, scale=0.125, layers=None, kv_scale=1.0):
+        """append + attend for each layer; returns [(layer, gpu_out, ref_out)]."""
+        g = torch.Generator().manual_seed(seed)
+        meta_gpu = _to_dev(meta_cpu)
+        T = meta_cpu.n_tokens
+        res = []
+        for layer in (layers if layers is not None else range(self.gpu.num_layers)):
+            k = self.rand((T, self.gpu.n_kv_heads, self.gpu.head_dim), g, kv_scale)
+            v = self.rand((T, self.gpu.n_kv_heads, self.gpu.head_dim), g, kv_scale)
+            q = self.rand((T, self.gpu.n_heads, self.gpu.head_dim), g)
+            self.gpu.append_kv(layer, k.to(DEV), v.to(DEV), meta_gpu)
+            out = self.gpu.attend(q.to(DEV), layer, scale, meta_gpu)
+            self.ref.append_kv(layer, k.float(), v.float(), meta_cpu)
+            want = self.ref.attend(q.float(), layer, scale, meta_cpu)
+            res.append((layer, out, want))
+        self.gpu.check_device_errors()
+        return res
+
+
+def _to_dev(meta):
+    return dataclasses.replace(meta, **{f.name: getattr(meta, f.name).to(DEV)
+                                        for f in dataclasses.fields(meta)
+                                        if isinstance(getattr(meta, f.name), torch.Tensor)})
+
+
+def check(res, label, atol=2e-3, rtol=1e-2):
+    for layer, got, want in res:
+        assert got.dtype == (got.dtype) and got.shape == want.shape
+        assert_attention_close(got, want, atol=atol, rtol=rtol, label=f"{label} layer {layer}")
+
+
+# ------------------------------------------------ the differential harness
+
+GEOMS = [
+    # (n_kv, n_heads, head_dim): bench geometry, the reference differential's, odd shapes
+    (8, 32, 64), (2, 8, 128), (8, 8, 64), (4, 8, 64), (1, 8, 64), (2, 4, 8),
+]
+
+
+@pytest.mark.parametrize("geom", GEOMS)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_then_decode_across_page_boundaries(geom, dtype):
+    n_kv, n_heads, d = geom
+    print(f"differential geom={geom} dtype={dtype}", flush=True)
+    p = Pair(2, 256, 16, n_kv, n_heads, d, dtype=dtype)
+    p.poison(1)
+    alloc, _keep = fragmented_allocator(256, 16)
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(5)]
+    tol = 2e-3 if dtype == torch.float16 else 1.6e-2  # bf16 rounds p to 8 bits
+    rtol = 1e-2 if dtype == torch.float16 else 8e-2
+    check(p.step(grow_and_assemble(seqs, [15, 16, 17, 1, 40], 16), 10), "prefill", tol, rtol)
+    for it in range(20):  # each sequence crosses at least one page boundary
+        check(p.step(grow_and_assemble(seqs, [1, 1, 1, 1, 1], 16), 100 + it), f"decode {it}",
+              tol, rtol)
+    check(p.step(grow_and_assemble(seqs, [1, 5, 0, 1, 9], 16), 7), "mixed", tol, rtol)
+
+
+@pytest.mark.parametrize("part_pages", [4, 8])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_long_sequences_split_k(part_pages, dtype):
+    """Sequences far longer than one partition: the split-K merge path."""
+    print(f"split-K decode part_pages={part_pages} dtype={dtype}", flush=True)
+    p = Pair(1, 512, 16, 8, 32, 64, dtype=dtype, part_pages=part_pages)
+    p.poison(2)
+    alloc, _keep = fragmented_allocator(512, 16)
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(6)]
+    for s, n in zip(seqs, [1, 63, 64, 65, 700, 1200]):
+        s.append(n)
+    meta = grow_and_assemble(seqs, [1] * 6, 16)
+    tol, rtol = (2e-3, 1e-2) if dtype == torch.float16 else (1.6e-2, 8e-2)
+    check(p.step(meta, 3), "split-K", tol, rtol)
+
+
+def test_config1_fp16_fast_path_and_fp32_fixture():
+    """The CPU plumbing case on the GPU: fp32 pools vs the golden float64
+    outputs, fp16 pools (fast decode kernel) vs the fp32 oracle."""
+    from .golden.make_config1 import build_inputs
+
+    print("config1 fp32 + fp16", flush=True)
+    fx = np.load(Path(__file__).resolve().parent / "golden" / "config1.npz", allow_pickle=False)
+    inp = build_inputs()
+    for dtype in (torch.float32, torch.float16):
+        bk = MI355XBackend(1, inp["num_blocks"], 16, 8, 32, 64, device=DEV, dtype=dtype)
+        hist, meta = _to_dev(inp["hist_meta"]), _to_dev(inp["meta"])
+        cast = lambda a: torch.from_numpy(a).to(DEV, dtype)  # noqa: E731
+        bk.append_kv(0, cast(inp["k_hist"]), cast(inp["v_hist"]), hist)
+        bk.append_kv(0, cast(inp["k_new"]), cast(inp["v_new"]), meta)
+        out = bk.attend(cast(inp["q"]), 0, 0.125, meta)
+        bk.check_device_errors()
+        if dtype == torch.float32:
+            np.testing.assert_allclose(out.cpu().numpy(), fx["out_f64"], atol=1e-5, rtol=1e-5)
+        else:
+            ref = PagedTorchOracle(1, inp["num_blocks"], 16, 8, 32, 64)
+            r = lambda a: torch.from_numpy(a).half().float()  # noqa: E731
+            ref.append_kv(0, r(inp["k_hist"]), r(inp["v_hist"]), inp["hist_meta"])
+            ref.append_kv(0, r(inp["k_new"]), r(inp["v_new"]), inp["meta"])
+            want = ref.attend(r(inp["q"]), 0, 0.125, inp["meta"])
+            assert_attention_close(out, want, label="config1 fp16")
+
+
+def test_config2_batch256_one_layer_vs_oracle():
+    """Full decode-bench batch (256 sequences, lognormal mean 258) on one layer."""
+    print("config2 batch 256 parity", flush=True)
+    lens = lognormal_lengths(256, 256, 0.8, 2048, 20260731)
+    pages = sum(-(-(n + 1) // 16) for n in lens)
+    nb = 2 * pages
+    p = Pair(2, nb, 16, 8, 32, 64)
+    g = torch.Generator().manual_seed(5)
+    perm = torch.randperm(nb, generator=g).tolist()
+    a = BlockAllocator(nb, 16)
+    a.allocate(nb)
+    a.free(perm)
+    seqs = [SequenceBlocks(a, seq_id=i) for i in range(256)]
+    hist = grow_and_assemble(seqs, lens, 16)
+    gk = torch.Generator().manual_seed(6)
+    T = hist.n_tokens
+    for layer in range(2):
+        k = (torch.randn(T, 8, 64, generator=gk) * 0.5).half()
+        v = (torch.randn(T, 8, 64, generator=gk) * 0.5).half()
+        p.gpu.append_kv(layer, k.to(DEV), v.to(DEV), _to_dev(hist))
+        p.ref.append_kv(layer, k.float(), v.float(), hist)
+    meta = grow_and_assemble(seqs, [1] * 256, 16)
+    check(p.step(meta, 8, kv_scale=0.5), "config2")
+
+
+# ------------------------------------------------------ known answers
+
+def small(dtype=torch.float16, n_kv=2, n_heads=4, d=64, bs=16, nb=32):
+    return MI355XBackend(1, nb, bs, n_kv, n_heads, d, device=DEV, dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_gqa_value_map_and_decode_sees_itself(dtype):
+    print(f"gqa value map dtype={dtype}", flush=True)
+    for n_kv, n_heads in ((2, 8), (8, 32), (1, 4)):
+        bk = small(dtype, n_kv, n_heads)
+        s = SequenceBlocks(BlockAllocator(32, 16))
+        s.append(1)
+        meta = make_meta([s], [1], 16, device=DEV)
+        v = torch.zeros(1, n_kv, 64, device=DEV, dtype=dtype)
+        for j in range(n_kv):
+            v[0, j] = j + 1.0
+        bk.append_kv(0, torch.zeros_like(v), v, meta)
+        out = bk.attend(torch.randn(1, n_heads, 64, device=DEV, dtype=dtype), 0, 1.0, meta)
+        groups = n_heads // n_kv
+        for h in range(n_heads):
+            assert torch.all(out[0, h] == h // groups + 1.0), (n_kv, n_heads, h)
+
+
+def test_gqa_key_map():
+    print("gqa key map", flush=True)
+    bk = small(torch.float16, 2, 8)
+    s = SequenceBlocks(BlockAllocator(32, 16))
+    s.append(2)
+    meta = make_meta([s], [2], 16, device=DEV)
+    k = torch.zeros(2, 2, 64, device=DEV, dtype=torch.float16)
+    v = torch.zeros_like(k)
+    for j in range(2):
+        k[0, j, j] = 50.0
+        k[1, j, 2 + j] = 50.0
+        v[0, j], v[1, j] = 1.0, -1.0
+    bk.append_kv(0, k, v, meta)
+    q = torch.zeros(2, 8, 64, device=DEV, dtype=torch.float16)
+    for h in range(8):
+        q[:, h, h // 4] = 1.0
+    out = bk.attend(q, 0, 1.0, meta)
+    assert (out[1, :, 0].float() > 0.99).all()
+
+
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 31, 32, 33])
+def test_block_straddle_poisoned_decode(n):
+    """The unwritten tail of the last page holds 1e3; reading it would be loud."""
+    print(f"straddle n={n}", flush=True)
+    p = Pair(1, 32, 16, 8, 32, 64)
+    p.gpu._pool.fill_(1e3)
+    for t in p.ref.k_pool + p.ref.v_pool:
+        t.fill_(1e3)
+    seqs = [SequenceBlocks(BlockAllocator(32, 16))]
+    if n > 1:  # history as one prefill chunk, then the decode step reaching kv_len n
+        check(p.step(grow_and_assemble(seqs, [n - 1], 16), 1), f"straddle prefill {n - 1}")
+    check(p.step(grow_and_assemble(seqs, [1], 16), 2), f"straddle decode {n}")
+
+
+def test_scattered_pages_equal_contiguous_and_batched_equals_solo():
+    print("bitwise page-order / batch invariance", flush=True)
+    g = torch.Generator().manual_seed(0)
+    k = torch.randn(300, 8, 64, generator=g).half().to(DEV)
+    v = torch.randn(300, 8, 64, generator=g).half().to(DEV)
+    q = torch.randn(3, 32, 64, generator=g).half().to(DEV)
+    outs = []
+    for frag in (False, True):
+        bk = MI355XBackend(1, 128, 16, 8, 32, 64, device=DEV)
+        a = BlockAllocator(128, 16)
+        if frag:
+            a.allocate(128)
+            a.free(list(range(127, 0, -3)))
+        seqs = [SequenceBlocks(a, seq_id=i) for i in range(3)]
+        lens = [100, 1, 199]
+        meta = make_meta_grow(seqs, lens, device=DEV)
+        bk.append_kv(0, k, v, meta)
+        dmeta = make_meta_grow(seqs, [1, 1, 1], device=DEV)
+        bk.append_kv(0, k[:3], v[:3], dmeta)
+        batched = bk.attend(q, 0, 0.125, dmeta)
+        outs.append(batched)
+        for i in range(3):
+            solo = bk.attend(q[i:i + 1], 0, 0.125, make_meta([seqs[i]], [1], 16, device=DEV))
+            assert torch.equal(solo, batched[i:i + 1]), f"seq {i} changed when batched"
+    assert torch.equal(outs[0], outs[1]), "physical page order changed the answer"
+
+
+def make_meta_grow(seqs, counts, device):
+    for s, n in zip(seqs, counts):
+        s.append(n)
+    return make_meta(seqs, counts, 16, device=device)
+
+
+def test_isolation_and_causality_prefill():
+    print("isolation + causality", flush=True)
+    bk = small(torch.float16, 2, 8, nb=64)
+    a = BlockAllocator(64, 16)
+    lens = [3, 1, 20]
+    seqs = [SequenceBlocks(a, seq_id=i) for i in range(3)]
+    meta = make_meta_grow(seqs, lens, device=DEV)
+    vs = torch.cat([torch.full((n, 2, 64), i + 1.0) for i, n in enumerate(lens)]).half().to(DEV)
+    bk.append_kv(0, torch.zeros_like(vs), vs, meta)
+    out = bk.attend(torch.randn(24, 8, 64, device=DEV).half(), 0, 1.0, meta)
+    cu = meta.cu_query_lens.tolist()
+    for i in range(3):
+        assert torch.all(out[cu[i]:cu[i + 1]] == i + 1.0)
+    # causality: poisoning the last key changes only the last query's output
+    s = [SequenceBlocks(a, seq_id=9)]
+    m = make_meta_grow(s, [6], device=DEV)
+    g = torch.Generator().manual_seed(3)
+    bk.append_kv(0, torch.randn(6, 2, 64, generator=g).half().to(DEV),
+                  torch.randn(6, 2, 64, generator=g).half().to(DEV), m)
+    q = torch.randn(6, 8, 64, generator=g).half().to(DEV)
+    base = bk.attend(q, 0, 0.125, m)
+    slot = s[0].slot_for(5)
+    bk.k_pool[0].view(-1, 2, 64)[slot] = 100.0
+    bk.v_pool[0].view(-1, 2, 64)[slot] = -999.0
+    pois = bk.attend(q, 0, 0.125, m)
+    assert torch.equal(base[:5], pois[:5])
+    assert not torch.allclose(base[5], pois[5])
+
+
+def test_plan_once_per_step_and_prefill_hint_checked():
+    print("plan caching + is_prefill cross-check", flush=True)
+    p = Pair(4, 64, 16, 8, 32, 64)
+    seqs = [SequenceBlocks(BlockAllocator(64, 16), seq_id=0)]
+    p.step(grow_and_assemble(seqs, [20], 16), 1)
+    assert p.gpu.n_plans == 1 and p.gpu.n_runs == 4
+    p.step(grow_and_assemble(seqs, [1], 16), 2)
+    assert p.gpu.n_plans == 2 and p.gpu.n_runs == 8
+    meta = _to_dev(grow_and_assemble(seqs, [1], 16))
+    bad = dataclasses.replace(meta, is_prefill=True)
+    with pytest.raises(ValueError, match="is_prefill"):
+        p.gpu.attend(torch.zeros(1, 32, 64, device=DEV, dtype=torch.float16), 0, 0.125, bad)
+
+
+def test_protocol_and_accounting():
+    from llm_serving_layer_amd import AttentionBackend
+
+    bk = MI355XBackend(16, 100, 16, 8, 32, 64, device=DEV)
+    assert isinstance(bk, AttentionBackend)
+    assert bk.block_bytes() == 512 * 1024
+    assert bk.pool_bytes() == 100 * 512 * 1024 == MI355XBackend.estimate_pool_bytes(16, 100, 16, 8, 64)
+    assert bk.tokens_capacity() == 1600
+    assert tuple(bk.zeros_like_pool().shape) == (100, 16, 8, 64)
+    for l in range(16):
+        assert bk.k_pool[l].is_contiguous() and bk.v_pool[l].is_contiguous()
+        assert tuple(bk.k_pool[l].shape) == (100, 16, 8, 64)

@@ -1,0 +1,145 @@
+"""
+The C-ABI boundary without a GPU: the library loads, exports exactly what
+include/pagedkv.h declares, and its host-side planners (pure CPU code) cover
+every page / query row exactly once and reject inconsistent metadata with the
+reference's messages (serving/backends/paged_torch.py:379-392).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import random
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from llm_serving_layer_amd import _native
+from llm_serving_layer_amd.backend import MI355XBackend
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "pagedkv.h"
+
+
+def ptr(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:const\s+)?[\w\*]+\s+\*?\s*(pkv_\w+)\s*\(", text, re.M))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    decl = declared_symbols()
+    assert decl == set(_native.SIGNATURES), "binding table and header disagree"
+    for name in decl:
+        assert hasattr(lib, name), f"{name} not exported"
+    assert lib.pkv_abi_version() == _native.ABI_VERSION
+
+
+def plan_decode(kv_lens, part_pages, ps=16):
+    n = len(kv_lens)
+    npages = [-(-k // ps) for k in kv_lens]
+    indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
+    kvl = np.array(kv_lens, np.int32)
+    last = np.array([k % ps or ps for k in kv_lens], np.int32)
+    cap = 4 * (int(indptr[-1]) + n) + 3 * n
+    buf = np.empty(cap, np.int32)
+    nw, nm, ns = C.c_int32(), C.c_int32(), C.c_int32()
+    rc = _native.load().pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), n, ps, part_pages,
+                                        ptr(buf), cap, C.byref(nw), C.byref(nm), C.byref(ns))
+    _native.check(rc, "plan")
+    work = buf[:4 * nw.value].reshape(-1, 4)
+    merges = buf[4 * nw.value:4 * nw.value + 3 * nm.value].reshape(-1, 3)
+    return npages, work, merges, ns.value
+
+
+@pytest.mark.parametrize("part_pages", [4, 8])
+def test_decode_plan_covers_every_page_once(part_pages):
+    rng = random.Random(part_pages)
+    kv_lens = [rng.randint(1, 700) for _ in range(300)] + [16, 64, 65, 1]
+    npages, work, merges, n_slots = plan_decode(kv_lens, part_pages)
+    covered = [[0] * p for p in npages]
+    slots = []
+    for seq, first, n, slot in work:
+        assert 1 <= n <= part_pages
+        for p in range(first, first + n):
+            covered[seq][p] += 1
+        if slot >= 0:
+            slots.append(slot)
+    assert all(all(c == 1 for c in row) for row in covered)
+    assert sorted(slots) == list(range(n_slots)), "partial slots must be dense and unique"
+    assert list(work[:, 2]) == sorted(work[:, 2], reverse=True), "longest partitions first"
+    split = {int(s) for s, _, k in merges if k > 1}
+    for i, p in enumerate(npages):
+        whole = [w for w in work if w[0] == i and w[3] < 0]
+        assert (p > part_pages) == (i in split) and (len(whole) == 1) == (p <= part_pages)
+    for seq, s0, k in merges:
+        assert k == -(-npages[seq] // part_pages)
+        own = sorted(int(w[3]) for w in work if w[0] == seq)
+        assert own == list(range(s0, s0 + k))
+
+
+def test_decode_plan_rejects_inconsistent_metadata():
+    lib = _native.load()
+    indptr = np.array([0, 1], np.int32)
+    out = np.empty(16, np.int32)
+    nw, nm, ns = C.c_int32(), C.c_int32(), C.c_int32()
+    kvl = np.array([16], np.int32)
+    last = np.array([9], np.int32)
+    rc = lib.pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), 1, 16, 4, ptr(out), 16,
+                             C.byref(nw), C.byref(nm), C.byref(ns))
+    with pytest.raises(ValueError, match="kv_last_page_len"):
+        _native.check(rc, "plan")
+    kvl[0] = 999
+    rc = lib.pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), 1, 16, 4, ptr(out), 16,
+                             C.byref(nw), C.byref(nm), C.byref(ns))
+    with pytest.raises(ValueError, match="pages supplied"):
+        _native.check(rc, "plan")
+
+
+def test_prefill_plan_covers_every_query_row_once():
+    lib = _native.load()
+    ql = [512, 1, 1, 77, 130]
+    kv = [2048, 300, 17, 77, 400]
+    n = len(ql)
+    cu = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
+    npages = [-(-k // 16) for k in kv]
+    indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
+    kvl = np.array(kv, np.int32)
+    last = np.array([k % 16 or 16 for k in kv], np.int32)
+    cap = 4 * (int(cu[-1]) // 64 + n + 1)
+    buf = np.empty(cap, np.int32)
+    nt = C.c_int32()
+    rc = lib.pkv_plan_prefill(ptr(cu), ptr(indptr), ptr(kvl), ptr(last), n, 16, 64, ptr(buf),
+                              cap, C.byref(nt))
+    _native.check(rc, "plan")
+    tiles = buf[:4 * nt.value].reshape(-1, 4)
+    seen = [[0] * q for q in ql]
+    for seq, q0, qn, _ in tiles:
+        assert 1 <= qn <= 64
+        for j in range(q0, q0 + qn):
+            seen[seq][j] += 1
+    assert all(all(c == 1 for c in row) for row in seen)
+
+
+def test_backend_validates_before_touching_the_library():
+    with pytest.raises(ValueError, match="divisible"):
+        MI355XBackend(1, 8, 16, 3, 4, 8)
+    with pytest.raises(ValueError, match="num_blocks must be positive"):
+        MI355XBackend(1, 0, 16, 2, 4, 8)
+    with pytest.raises(ValueError, match="supports"):
+        MI355XBackend(1, 8, 16, 2, 4, 8, dtype=torch.float64)
+    with pytest.raises(ValueError, match="GPU device"):
+        MI355XBackend(1, 8, 16, 2, 4, 8, device="cpu")
+
+
+def test_error_codes_map_to_reference_exception_types():
+    lib = _native.load()
+    rc = lib.pkv_copy_blocks(None, 0, 0, 0, 0, None, None, 1, None, None)
+    with pytest.raises(ValueError):
+        _native.check(rc, "copy")
+    assert lib.pkv_last_error()
