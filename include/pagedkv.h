@@ -77,20 +77,22 @@ int pkv_append_kv(void* k_pool, void* v_pool, int64_t num_slots,
  * that kv_last_page_len agrees (PKV_ERR_INVALID, message naming
  * kv_last_page_len, as serving/backends/paged_torch.py:379-392 does).
  *
- * Output `plan` (int32), capacity `plan_capacity` entries:
- *   [0 .. 4*n_work)            work items {seq, first_page, n_pages, slot}
- *                              (slot = -1: the item covers the whole sequence)
- *   [4*n_work .. +3*n_merge)   merge items {seq, first_slot, n_slots}
- * *n_slots_out is the number of partial-result slots the workspace must hold.
+ * Output `plan` (int32):
+ *   [0 .. 8*n_work)  work items {seq, first index into kv_indices, n_pages,
+ *                    partial slot (-1: the item covers the whole sequence),
+ *                    kv_len, first token, n_parts, first slot}
+ *   then 3 entries per split sequence {seq, first slot, n_slots}
+ * *n_split_out: sequences cut into more than one partition (merge items);
+ * *n_slots_out: partial-result slots the workspace must hold.
  */
 int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_lens,
                     const int32_t* kv_last_page_len, int32_t n_seqs,
                     int32_t page_size, int32_t part_pages,
                     int32_t* plan, int64_t plan_capacity,
-                    int32_t* n_work_out, int32_t* n_merge_out,
+                    int32_t* n_work_out, int32_t* n_split_out,
                     int32_t* n_slots_out);
 
-/* Bytes of workspace pkv_attend_decode needs for `n_slots` partial slots. */
+/* Bytes of workspace pkv_attend_decode needs for `n_slots` partial results. */
 int64_t pkv_decode_workspace_bytes(int32_t n_slots, int32_t n_heads, int32_t head_dim);
 
 /*
@@ -101,7 +103,12 @@ int64_t pkv_decode_workspace_bytes(int32_t n_slots, int32_t n_heads, int32_t hea
  * (token i belongs to sequence i). q, out: [n_seqs, n_heads, head_dim];
  * query head h reads KV head h / (n_heads / n_kv_heads); no mask (the
  * single query is the last position). `plan` is the device copy of
- * pkv_plan_decode's output; `workspace` holds the split-K partials.
+ * pkv_plan_decode's output; split sequences write partials to `workspace`
+ * and a second small kernel in the same call merges them. Launches that
+ * share a workspace must not overlap in time (same stream is fine).
+ * Geometries outside the fast kernel (head_dim not 64/128, more than 4
+ * query heads per KV head, page_size != 16, fp32) run the generic kernel,
+ * which reads kv_indptr/kv_lens instead of the plan.
  */
 int pkv_attend_decode(const void* q, void* out,
                       const void* k_pool, const void* v_pool, int64_t num_blocks,

@@ -12,7 +12,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_native" / "libpagedkv.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 OK, ERR_INVALID, ERR_RANGE, ERR_HIP, ERR_CAPACITY = 0, 1, 2, 3, 4

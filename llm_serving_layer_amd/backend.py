@@ -333,13 +333,13 @@ class MI355XBackend:
                              f"for {p.n_tokens} tokens")
         n_work, n_merge, n_slots = C.c_int32(), C.c_int32(), C.c_int32()
         if not use_prefill:
-            cap = 4 * (int(indptr[-1]) + n) + 3 * n
-            buf = np.empty(max(cap, 4), dtype=np.int32)
+            cap = 8 * (int(indptr[-1]) + n) + 3 * n
+            buf = np.empty(cap, dtype=np.int32)
             rc = self._lib.pkv_plan_decode(ptr(indptr32), ptr(kvl32), ptr(last32), n,
                                            self.block_size, self.part_pages, ptr(buf), cap,
                                            C.byref(n_work), C.byref(n_merge), C.byref(n_slots))
             _native.check(rc, "plan (decode)")
-            used = 4 * n_work.value + 3 * n_merge.value
+            used = 8 * n_work.value + 3 * n_merge.value
             p.n_work, p.n_merge, p.n_slots = n_work.value, n_merge.value, n_slots.value
             need = self._lib.pkv_decode_workspace_bytes(p.n_slots, self.n_heads, self.head_dim)
             if need > self._workspace.numel():

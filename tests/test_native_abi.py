@@ -46,41 +46,43 @@ def plan_decode(kv_lens, part_pages, ps=16):
     indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
     kvl = np.array(kv_lens, np.int32)
     last = np.array([k % ps or ps for k in kv_lens], np.int32)
-    cap = 4 * (int(indptr[-1]) + n) + 3 * n
+    cap = 8 * (int(indptr[-1]) + n) + 3 * n
     buf = np.empty(cap, np.int32)
-    nw, nm, ns = C.c_int32(), C.c_int32(), C.c_int32()
+    nw, nsplit, ns = C.c_int32(), C.c_int32(), C.c_int32()
     rc = _native.load().pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), n, ps, part_pages,
-                                        ptr(buf), cap, C.byref(nw), C.byref(nm), C.byref(ns))
+                                        ptr(buf), cap, C.byref(nw), C.byref(nsplit), C.byref(ns))
     _native.check(rc, "plan")
-    work = buf[:4 * nw.value].reshape(-1, 4)
-    merges = buf[4 * nw.value:4 * nw.value + 3 * nm.value].reshape(-1, 3)
-    return npages, work, merges, ns.value
+    work = buf[:8 * nw.value].reshape(-1, 8)
+    merges = buf[8 * nw.value:8 * nw.value + 3 * nsplit.value].reshape(-1, 3)
+    return indptr, npages, work, merges, ns.value
 
 
-@pytest.mark.parametrize("part_pages", [4, 8])
+@pytest.mark.parametrize("part_pages", [2, 4, 8])
 def test_decode_plan_covers_every_page_once(part_pages):
     rng = random.Random(part_pages)
     kv_lens = [rng.randint(1, 700) for _ in range(300)] + [16, 64, 65, 1]
-    npages, work, merges, n_slots = plan_decode(kv_lens, part_pages)
+    indptr, npages, work, merges, n_slots = plan_decode(kv_lens, part_pages)
     covered = [[0] * p for p in npages]
     slots = []
-    for seq, first, n, slot in work:
-        assert 1 <= n <= part_pages
+    for seq, pbase, n, slot, kv, tok0, nparts, slot0 in work:
+        assert 1 <= n <= part_pages and kv == kv_lens[seq]
+        first = pbase - indptr[seq]
+        assert tok0 == first * 16 and 0 <= first and first + n <= npages[seq]
+        assert nparts == -(-npages[seq] // part_pages)
         for p in range(first, first + n):
             covered[seq][p] += 1
-        if slot >= 0:
+        if nparts == 1:
+            assert slot == -1 and slot0 == -1
+        else:
+            assert slot0 <= slot < slot0 + nparts and slot - slot0 == first // part_pages
             slots.append(slot)
     assert all(all(c == 1 for c in row) for row in covered)
     assert sorted(slots) == list(range(n_slots)), "partial slots must be dense and unique"
     assert list(work[:, 2]) == sorted(work[:, 2], reverse=True), "longest partitions first"
-    split = {int(s) for s, _, k in merges if k > 1}
-    for i, p in enumerate(npages):
-        whole = [w for w in work if w[0] == i and w[3] < 0]
-        assert (p > part_pages) == (i in split) and (len(whole) == 1) == (p <= part_pages)
+    assert len(merges) == sum(1 for p in npages if p > part_pages)
     for seq, s0, k in merges:
         assert k == -(-npages[seq] // part_pages)
-        own = sorted(int(w[3]) for w in work if w[0] == seq)
-        assert own == list(range(s0, s0 + k))
+        assert sorted(int(w[3]) for w in work if w[0] == seq) == list(range(s0, s0 + k))
 
 
 def test_decode_plan_rejects_inconsistent_metadata():
