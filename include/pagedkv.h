@@ -77,23 +77,32 @@ int pkv_append_kv(void* k_pool, void* v_pool, int64_t num_slots,
  * that kv_last_page_len agrees (PKV_ERR_INVALID, message naming
  * kv_last_page_len, as serving/backends/paged_torch.py:379-392 does).
  *
- * Output `plan` (int32):
- *   [0 .. 8*n_work)  work items {seq, first index into kv_indices, n_pages,
- *                    partial slot (-1: the item covers the whole sequence),
- *                    kv_len, first token, n_parts, first slot}
- *   then 3 entries per split sequence {seq, first slot, n_slots}
- * *n_split_out: sequences cut into more than one partition (merge items);
- * *n_slots_out: partial-result slots the workspace must hold.
+ * Output `plan` (int32), 8 entries per partition:
+ *   {seq, index of its first page in kv_indices, n_pages, partial slot
+ *    (-1: the partition is the whole sequence), kv_len, first token,
+ *    n_partitions of the sequence, first slot of the sequence}
+ * *n_slots_out: partial-result slots of split sequences (workspace size).
  */
 int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_lens,
                     const int32_t* kv_last_page_len, int32_t n_seqs,
                     int32_t page_size, int32_t part_pages,
                     int32_t* plan, int64_t plan_capacity,
-                    int32_t* n_work_out, int32_t* n_split_out,
-                    int32_t* n_slots_out);
+                    int32_t* n_work_out, int32_t* n_slots_out);
 
-/* Bytes of workspace pkv_attend_decode needs for `n_slots` partial results. */
-int64_t pkv_decode_workspace_bytes(int32_t n_slots, int32_t n_heads, int32_t head_dim);
+/*
+ * Bytes of workspace pkv_attend_decode needs: arrival counters for
+ * n_seqs * n_kv_heads (zero before the first launch that uses the workspace;
+ * every launch leaves them zero) then n_slots partial results.
+ */
+int64_t pkv_decode_workspace_bytes(int32_t n_seqs, int32_t n_slots, int32_t n_heads,
+                                   int32_t n_kv_heads, int32_t head_dim);
+
+/*
+ * 1 if pkv_attend_decode runs its fast kernel for this geometry (and so
+ * accepts a fused append), 0 if it falls back to the generic kernel.
+ */
+int pkv_decode_fast_path(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                         int32_t page_size, int32_t dtype, int32_t part_pages);
 
 /*
  * Paged decode attention — replaces PagedTorchBackend.attend
@@ -103,21 +112,28 @@ int64_t pkv_decode_workspace_bytes(int32_t n_slots, int32_t n_heads, int32_t hea
  * (token i belongs to sequence i). q, out: [n_seqs, n_heads, head_dim];
  * query head h reads KV head h / (n_heads / n_kv_heads); no mask (the
  * single query is the last position). `plan` is the device copy of
- * pkv_plan_decode's output; split sequences write partials to `workspace`
- * and a second small kernel in the same call merges them. Launches that
- * share a workspace must not overlap in time (same stream is fine).
- * Geometries outside the fast kernel (head_dim not 64/128, more than 4
+ * pkv_plan_decode's output. Split sequences merge inside the launch through
+ * `workspace` (256-byte aligned, pkv_decode_workspace_bytes long); launches
+ * that share a workspace must not overlap in time (same stream is fine).
+ *
+ * Fused append: if k_new / v_new ([n_seqs, n_kv_heads, head_dim]) and
+ * slot_mapping ([n_seqs]) are given, the launch also performs pkv_append_kv
+ * of those rows, with the same result as the two calls in sequence (fast
+ * path only). Pass NULL for all three otherwise.
+ *
+ * Geometries outside the fast kernel (head_dim not 64/128, more than 16
  * query heads per KV head, page_size != 16, fp32) run the generic kernel,
- * which reads kv_indptr/kv_lens instead of the plan.
+ * which reads kv_indptr / kv_lens instead of the plan.
  */
 int pkv_attend_decode(const void* q, void* out,
-                      const void* k_pool, const void* v_pool, int64_t num_blocks,
+                      void* k_pool, void* v_pool, int64_t num_blocks,
                       const int32_t* kv_indptr, const int32_t* kv_indices,
                       const int32_t* kv_lens, int32_t n_seqs,
                       int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                       int32_t page_size, float scale, int32_t dtype,
-                      const int32_t* plan, int32_t n_work, int32_t n_merge,
-                      int32_t n_slots, int32_t part_pages,
+                      const int32_t* plan, int32_t n_work, int32_t n_slots,
+                      int32_t part_pages,
+                      const void* k_new, const void* v_new, const int32_t* slot_mapping,
                       void* workspace, int64_t workspace_bytes,
                       int32_t* status_word, void* stream);
 

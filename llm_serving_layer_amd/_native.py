@@ -9,10 +9,13 @@ The library is built in-tree (``python -m llm_serving_layer_amd.build``) into
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "_native" / "libpagedkv.so"
-ABI_VERSION = 2
+# PKV_LIBRARY selects another build of the same library (e.g. a tuning variant).
+LIB_PATH = Path(os.environ.get("PKV_LIBRARY") or
+                Path(__file__).resolve().parent / "_native" / "libpagedkv.so")
+ABI_VERSION = 4
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 OK, ERR_INVALID, ERR_RANGE, ERR_HIP, ERR_CAPACITY = 0, 1, 2, 3, 4
@@ -25,11 +28,12 @@ SIGNATURES = {
     "pkv_abi_version": (C.c_int, []),
     "pkv_last_error": (C.c_char_p, []),
     "pkv_append_kv": (C.c_int, [_p, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i32, _p, _p]),
-    "pkv_plan_decode": (C.c_int, [_p, _p, _p, _i32, _i32, _i32, _p, _i64, _p, _p, _p]),
-    "pkv_decode_workspace_bytes": (C.c_int64, [_i32, _i32, _i32]),
+    "pkv_plan_decode": (C.c_int, [_p, _p, _p, _i32, _i32, _i32, _p, _i64, _p, _p]),
+    "pkv_decode_workspace_bytes": (C.c_int64, [_i32, _i32, _i32, _i32, _i32]),
+    "pkv_decode_fast_path": (C.c_int, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "pkv_attend_decode": (C.c_int, [_p, _p, _p, _p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32,
-                                    _i32, _f32, _i32, _p, _i32, _i32, _i32, _i32, _p, _i64,
-                                    _p, _p]),
+                                    _i32, _f32, _i32, _p, _i32, _i32, _i32, _p, _p, _p, _p,
+                                    _i64, _p, _p]),
     "pkv_plan_prefill": (C.c_int, [_p, _p, _p, _p, _i32, _i32, _i32, _p, _i64, _p]),
     "pkv_attend_prefill": (C.c_int, [_p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _i32, _i32,
                                      _i32, _i32, _i32, _i32, _f32, _i32, _p, _i32, _i32, _p,

@@ -20,8 +20,18 @@ Drop-in surface (same as both reference backends):
   (paged_torch.py:139-207), plus ``workspace_bytes()``, ``invalidate_plan()``
   and the ``n_plans`` / ``n_runs`` counters (flashinfer_backend.py:354-394,
   678-688);
-* plan once per ``BatchMeta`` identity and scale, run once per layer
+* plan once per ``BatchMeta`` identity, run once per layer
   (flashinfer_backend.py:566-676), including the ``is_prefill`` cross-check.
+
+One launch per layer on decode steps: for a decode-shaped batch on the fast
+geometry, ``append_kv`` records its rows and the following ``attend`` of the
+same layer performs the append inside the attention kernel (the result is
+exactly append-then-attend). Anything else that could observe the pool --
+reading ``k_pool`` / ``v_pool``, another append or attend, ``copy_block(s)``,
+``reset``, swapping, ``check_device_errors`` -- first launches the recorded
+append on its own. A caller must not modify ``k`` / ``v`` in place between
+``append_kv`` and the next backend call; that is detected (tensor version
+counters) and raises.
 
 Everything runs on torch's current stream of the backend's device. Not
 thread-safe and not re-entrant, like the reference backends.
@@ -55,16 +65,21 @@ def unavailable_reason() -> str | None:
     return _native.reason()
 
 
-def _ptr(t: torch.Tensor | None) -> int | None:
-    return None if t is None else t.data_ptr()
+def _current_stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 class _Plan:
     """Device-side metadata and launch plan for one BatchMeta (one step)."""
 
-    __slots__ = ("meta", "scale", "use_prefill", "slots", "indptr", "indices", "kv_lens",
-                 "cu_q", "bidx", "plan", "n_work", "n_merge", "n_slots", "n_tokens",
-                 "n_seqs")
+    __slots__ = ("meta", "use_prefill", "slots", "indptr", "indices", "kv_lens", "cu_q",
+                 "bidx", "plan", "n_work", "n_slots", "n_tokens", "n_seqs")
+
+
+class _Pending:
+    """An append_kv whose rows will be written by the next launch."""
+
+    __slots__ = ("layer", "k", "v", "meta", "slots", "stream", "kver", "vver")
 
 
 class MI355XBackend:
@@ -73,7 +88,8 @@ class MI355XBackend:
     def __init__(self, num_layers: int, num_blocks: int, block_size: int, n_kv_heads: int,
                  n_heads: int, head_dim: int, device: str | torch.device = "cuda:0",
                  dtype: torch.dtype = torch.float16, *,
-                 part_pages: int = DEFAULT_PART_PAGES, q_tile: int = DEFAULT_Q_TILE):
+                 part_pages: int = DEFAULT_PART_PAGES, q_tile: int = DEFAULT_Q_TILE,
+                 fuse_append: bool = True):
         if n_heads % n_kv_heads != 0:
             raise ValueError(
                 f"n_heads={n_heads} must be divisible by n_kv_heads={n_kv_heads}; "
@@ -112,24 +128,40 @@ class MI355XBackend:
         self.part_pages = part_pages
         self.q_tile = q_tile
         self._code = _DTYPES[dtype]
+        self._fast_decode = bool(self._lib.pkv_decode_fast_path(
+            n_heads, n_kv_heads, head_dim, block_size, self._code, part_pages))
+        self._fuse_append = fuse_append and self._fast_decode
 
         self._pool = torch.zeros((num_layers, 2, num_blocks, block_size, n_kv_heads, head_dim),
                                  dtype=dtype, device=self.device)
-        self.k_pool: list[torch.Tensor] = [self._pool[l, 0] for l in range(num_layers)]
-        self.v_pool: list[torch.Tensor] = [self._pool[l, 1] for l in range(num_layers)]
+        self._k_pool = [self._pool[l, 0] for l in range(num_layers)]
+        self._v_pool = [self._pool[l, 1] for l in range(num_layers)]
         self._block_bytes = block_size * n_kv_heads * head_dim * self._pool.element_size()
         self._plane_bytes = num_blocks * self._block_bytes
         self._status = torch.zeros(1, dtype=torch.int32, device=self.device)
-        self._workspace = torch.empty(0, dtype=torch.uint8, device=self.device)
+        self._workspace = torch.zeros(0, dtype=torch.uint8, device=self.device)
         self._planned: _Plan | None = None
         self._slot_cache: tuple[BatchMeta, torch.Tensor] | None = None
+        self._pending: _Pending | None = None
         self.n_plans = 0
         self.n_runs = 0
+
+    # -- the pools (reading them first lands any deferred append) ---------------
+
+    @property
+    def k_pool(self) -> list[torch.Tensor]:
+        self._flush()
+        return self._k_pool
+
+    @property
+    def v_pool(self) -> list[torch.Tensor]:
+        self._flush()
+        return self._v_pool
 
     # -- pool construction / accounting ---------------------------------------
 
     def zeros_like_pool(self) -> torch.Tensor:
-        return torch.zeros_like(self.k_pool[0])
+        return torch.zeros_like(self._k_pool[0])
 
     def pool_bytes(self) -> int:
         return self.num_layers * 2 * self._plane_bytes
@@ -138,7 +170,8 @@ class MI355XBackend:
         return self.pool_bytes() // self.num_blocks
 
     def workspace_bytes(self) -> int:
-        """Split-K partials; grows with the largest batch planned, not with the pool."""
+        """Split-K partials and arrival counters; grows with the largest batch
+        planned, not with the pool."""
         return self._workspace.numel()
 
     def tokens_capacity(self) -> int:
@@ -152,9 +185,6 @@ class MI355XBackend:
         return num_layers * 2 * num_blocks * block_size * n_kv_heads * head_dim * elem
 
     # -- helpers -----------------------------------------------------------------
-
-    def _stream(self) -> int:
-        return torch.cuda.current_stream(self.device).cuda_stream
 
     def _check_layer(self, layer_idx) -> None:
         if layer_idx is None or not 0 <= layer_idx < self.num_layers:
@@ -171,6 +201,7 @@ class MI355XBackend:
         Declared check point: synchronise and raise if any kernel since the
         last check skipped an out-of-range slot, page or block id.
         """
+        self._flush()
         bits = int(self._status.item())
         if bits:
             self._status.zero_()
@@ -212,12 +243,13 @@ class MI355XBackend:
         ds = [d for _, d in pairs]
         if len(set(ds)) != len(ds) or set(ds) & {s for s, _ in pairs}:
             raise ValueError("copy_blocks needs distinct destinations that are not also sources")
+        self._flush()
         ids = torch.tensor([s for s, _ in pairs] + ds, dtype=torch.int32).to(self.device)
         n = len(pairs)
         rc = self._lib.pkv_copy_blocks(self._pool.data_ptr(), self.num_layers,
                                        self._plane_bytes, self._block_bytes, self.num_blocks,
                                        ids.data_ptr(), ids.data_ptr() + 4 * n, n,
-                                       self._status.data_ptr(), self._stream())
+                                       self._status.data_ptr(), _current_stream(self.device))
         _native.check(rc, "copy_blocks")
 
     def append_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor,
@@ -235,20 +267,64 @@ class MI355XBackend:
         if meta.slot_mapping.shape[0] != tokens:
             raise ValueError(f"slot_mapping has {meta.slot_mapping.shape[0]} entries but "
                              f"{tokens} tokens were supplied")
-        sc = self._slot_cache
-        if sc is not None and sc[0] is meta:
-            slots = sc[1]
-        else:
-            slots = self._dev_i32(meta.slot_mapping)
-            self._slot_cache = (meta, slots)
+        self._flush()
         k = self._as_pool(k)
         v = self._as_pool(v)
+        stream = _current_stream(self.device)
+        if self._fuse_append:
+            try:
+                p = self._ensure_planned(meta)
+            except ValueError:
+                p = None  # inconsistent paging metadata: append now, attend will raise
+            if p is not None and not p.use_prefill:
+                pend = _Pending()
+                pend.layer, pend.k, pend.v, pend.meta = layer_idx, k, v, meta
+                pend.slots, pend.stream = p.slots, stream
+                pend.kver, pend.vver = k._version, v._version
+                self._pending = pend
+                return
+        self._launch_append(layer_idx, k, v, self._slots_for(meta), stream)
+
+    def _slots_for(self, meta: BatchMeta) -> torch.Tensor:
+        p = self._planned
+        if p is not None and p.meta is meta:
+            return p.slots
+        sc = self._slot_cache
+        if sc is not None and sc[0] is meta:
+            return sc[1]
+        slots = self._dev_i32(meta.slot_mapping)
+        self._slot_cache = (meta, slots)
+        return slots
+
+    def _launch_append(self, layer, k, v, slots, stream) -> None:
         rc = self._lib.pkv_append_kv(
-            self.k_pool[layer_idx].data_ptr(), self.v_pool[layer_idx].data_ptr(),
+            self._k_pool[layer].data_ptr(), self._v_pool[layer].data_ptr(),
             self.num_blocks * self.block_size, k.data_ptr(), v.data_ptr(), slots.data_ptr(),
-            tokens, self.n_kv_heads, self.head_dim, self._code, self._status.data_ptr(),
-            self._stream())
+            k.shape[0], self.n_kv_heads, self.head_dim, self._code, self._status.data_ptr(),
+            stream)
         _native.check(rc, "append_kv")
+
+    def _check_pending_intact(self, pend: _Pending) -> None:
+        if pend.k._version != pend.kver or pend.v._version != pend.vver:
+            self._pending = None
+            raise RuntimeError(
+                "k/v passed to append_kv were modified in place before the rows were "
+                "written; pass tensors that stay unchanged until the next backend call"
+            )
+
+    def _flush(self) -> None:
+        """Launch a deferred append on its own (on the stream it was issued on)."""
+        pend = self._pending
+        if pend is None:
+            return
+        self._check_pending_intact(pend)
+        self._pending = None
+        self._launch_append(pend.layer, pend.k, pend.v, pend.slots, pend.stream)
+        cur = _current_stream(self.device)
+        if cur != pend.stream:  # later work on this stream must see the rows
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.ExternalStream(pend.stream, device=self.device))
+            torch.cuda.current_stream(self.device).wait_event(ev)
 
     # -- read path ------------------------------------------------------------------
 
@@ -262,11 +338,20 @@ class MI355XBackend:
                              f"({tokens}, {self.n_heads}, {self.head_dim})")
         if meta.n_tokens != tokens:
             raise ValueError(f"meta describes {meta.n_tokens} tokens but q has {tokens}")
-        p = self._ensure_planned(meta, scale)
+        p = self._ensure_planned(meta)
+        stream = _current_stream(self.device)
+        pend = self._pending
+        fused = (pend is not None and pend.layer == layer_idx and pend.meta is meta
+                 and pend.stream == stream and not p.use_prefill)
+        if fused:
+            self._check_pending_intact(pend)
+            self._pending = None
+        else:
+            self._flush()
         q = self._as_pool(q)
         out = torch.empty_like(q)
-        kp = self.k_pool[layer_idx].data_ptr()
-        vp = self.v_pool[layer_idx].data_ptr()
+        kp = self._k_pool[layer_idx].data_ptr()
+        vp = self._v_pool[layer_idx].data_ptr()
         self.n_runs += 1
         if not p.use_prefill:
             ws = self._workspace
@@ -274,9 +359,11 @@ class MI355XBackend:
                 q.data_ptr(), out.data_ptr(), kp, vp, self.num_blocks, p.indptr.data_ptr(),
                 p.indices.data_ptr(), p.kv_lens.data_ptr(), p.n_seqs, self.n_heads,
                 self.n_kv_heads, self.head_dim, self.block_size, float(scale), self._code,
-                p.plan.data_ptr(), p.n_work, p.n_merge, p.n_slots, self.part_pages,
+                p.plan.data_ptr(), p.n_work, p.n_slots, self.part_pages,
+                pend.k.data_ptr() if fused else None, pend.v.data_ptr() if fused else None,
+                p.slots.data_ptr() if fused else None,
                 ws.data_ptr() if ws.numel() else None, ws.numel(), self._status.data_ptr(),
-                self._stream())
+                stream)
             _native.check(rc, "attend (decode)")
         else:
             rc = self._lib.pkv_attend_prefill(
@@ -284,20 +371,21 @@ class MI355XBackend:
                 p.indptr.data_ptr(), p.indices.data_ptr(), p.kv_lens.data_ptr(),
                 p.bidx.data_ptr(), p.n_seqs, p.n_tokens, self.n_heads, self.n_kv_heads,
                 self.head_dim, self.block_size, float(scale), self._code, p.plan.data_ptr(),
-                p.n_work, self.q_tile, self._status.data_ptr(), self._stream())
+                p.n_work, self.q_tile, self._status.data_ptr(), stream)
             _native.check(rc, "attend (prefill)")
         return out
 
     # -- planning ---------------------------------------------------------------
 
-    def _ensure_planned(self, meta: BatchMeta, scale: float) -> _Plan:
+    def _ensure_planned(self, meta: BatchMeta) -> _Plan:
         """
         Build the launch plan for ``meta`` at most once per forward pass.
-        Keyed on the object identity of the (frozen) BatchMeta plus the scale,
-        with a strong reference held so the identity cannot be recycled.
+        Keyed on the object identity of the (frozen) BatchMeta, with a strong
+        reference held so the identity cannot be recycled. The softmax scale
+        is a launch argument, not part of the plan.
         """
         pl = self._planned
-        if pl is not None and pl.meta is meta and pl.scale == scale:
+        if pl is not None and pl.meta is meta:
             return pl
         n = meta.n_seqs
         # ONE device->host transfer for everything the host plan reads.
@@ -316,11 +404,8 @@ class MI355XBackend:
                 f"(max={int(ql.max())}). is_prefill must be True iff some sequence "
                 "contributes more than one token."
             )
-        i32 = lambda a: np.ascontiguousarray(a, dtype=np.int32)  # noqa: E731
-        kvl32, indptr32, last32, cu32 = i32(kvl), i32(indptr), i32(last), i32(cu)
-        ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
         p = _Plan()
-        p.meta, p.scale, p.use_prefill = meta, scale, use_prefill
+        p.meta, p.use_prefill = meta, use_prefill
         p.n_seqs, p.n_tokens = n, int(cu[-1])
         if p.n_tokens != meta.n_tokens:
             raise ValueError(f"cu_query_lens ends at {p.n_tokens} but meta has "
@@ -331,19 +416,27 @@ class MI355XBackend:
         if int(meta.batch_indices.shape[0]) != p.n_tokens:
             raise ValueError(f"batch_indices has {int(meta.batch_indices.shape[0])} entries "
                              f"for {p.n_tokens} tokens")
-        n_work, n_merge, n_slots = C.c_int32(), C.c_int32(), C.c_int32()
+        i32 = lambda a: np.ascontiguousarray(a, dtype=np.int32)  # noqa: E731
+        kvl32, indptr32, last32, cu32 = i32(kvl), i32(indptr), i32(last), i32(cu)
+        ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
+        n_work, n_slots = C.c_int32(), C.c_int32()
         if not use_prefill:
-            cap = 8 * (int(indptr[-1]) + n) + 3 * n
+            cap = 8 * (int(indptr[-1]) + n)
             buf = np.empty(cap, dtype=np.int32)
             rc = self._lib.pkv_plan_decode(ptr(indptr32), ptr(kvl32), ptr(last32), n,
                                            self.block_size, self.part_pages, ptr(buf), cap,
-                                           C.byref(n_work), C.byref(n_merge), C.byref(n_slots))
+                                           C.byref(n_work), C.byref(n_slots))
             _native.check(rc, "plan (decode)")
-            used = 8 * n_work.value + 3 * n_merge.value
-            p.n_work, p.n_merge, p.n_slots = n_work.value, n_merge.value, n_slots.value
-            need = self._lib.pkv_decode_workspace_bytes(p.n_slots, self.n_heads, self.head_dim)
+            used = 8 * n_work.value
+            need = self._lib.pkv_decode_workspace_bytes(n, n_slots.value, self.n_heads,
+                                                        self.n_kv_heads, self.head_dim)
             if need > self._workspace.numel():
-                self._workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
+                # zero-filled: the arrival counters at the front start at zero
+                self._workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)
+            elif need > 0:
+                # a previous layout may have left partial data where counters now sit
+                counter_bytes = (4 * n * self.n_kv_heads + 255) // 256 * 256
+                self._workspace[:counter_bytes].zero_()
         else:
             cap = 4 * (int(cu[-1]) // self.q_tile + n + 1)
             buf = np.empty(cap, dtype=np.int32)
@@ -352,19 +445,22 @@ class MI355XBackend:
                                             C.byref(n_work))
             _native.check(rc, "plan (prefill)")
             used = 4 * n_work.value
-            p.n_work, p.n_merge, p.n_slots = n_work.value, 0, 0
+        p.n_work, p.n_slots = n_work.value, n_slots.value
         p.plan = torch.from_numpy(buf[:used].copy()).to(self.device)
         p.indptr = self._dev_i32(meta.kv_indptr)
         p.indices = self._dev_i32(meta.kv_indices)
         p.kv_lens = self._dev_i32(meta.kv_lens)
         p.cu_q = self._dev_i32(meta.cu_query_lens)
         p.bidx = self._dev_i32(meta.batch_indices)
+        p.slots = (self._dev_i32(meta.slot_mapping) if meta.slot_mapping is not None
+                   else None)
         self._planned = p
         self.n_plans += 1
         return p
 
     def invalidate_plan(self) -> None:
         """Force the next ``attend`` to re-plan (and drop the cached meta)."""
+        self._flush()
         self._planned = None
         self._slot_cache = None
 
@@ -372,6 +468,7 @@ class MI355XBackend:
 
     def reset(self) -> None:
         """Zero every pool and drop the plan. Tests only."""
+        self._pending = None
         self._pool.zero_()
         self.invalidate_plan()
 

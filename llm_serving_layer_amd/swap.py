@@ -137,6 +137,7 @@ class KVSwapSpace:
                                 f"of {self.max_bytes} B host swap space already in use")
         t0 = time.perf_counter()
         b = self.backend
+        b._flush()  # a deferred append must land before the blocks are read
         host = torch.empty(self._shape(nb), dtype=self.dtype, pin_memory=True)
         done = staging = None
         if nb:
@@ -186,6 +187,7 @@ class KVSwapSpace:
         if len(set(blocks.block_ids)) != nb:
             raise RuntimeError("swap_in target block ids must be distinct")
         b = self.backend
+        b._flush()
         main = torch.cuda.current_stream(self.device)
         ids = self._ids(blocks.block_ids)
         side = self._side

@@ -323,3 +323,90 @@ def test_protocol_and_accounting():
     for l in range(16):
         assert bk.k_pool[l].is_contiguous() and bk.v_pool[l].is_contiguous()
         assert tuple(bk.k_pool[l].shape) == (100, 16, 8, 64)
+
+
+# ------------------------------------------- one launch per layer (fused append)
+
+def _decode_batch(nb, lens, seed):
+    a = BlockAllocator(nb, 16)
+    a.allocate(nb)
+    a.free(torch.randperm(nb, generator=torch.Generator().manual_seed(seed)).tolist())
+    seqs = [SequenceBlocks(a, seq_id=i) for i in range(len(lens))]
+    return seqs, grow_and_assemble(seqs, lens, 16)
+
+
+@pytest.mark.parametrize("part_pages", [2, 4, 8])
+def test_fused_append_equals_separate_launches(part_pages):
+    """Deferred append fused into attend == append kernel then attend, bitwise."""
+    print(f"fused vs separate part_pages={part_pages}", flush=True)
+    lens = [1, 15, 16, 17, 63, 64, 65, 200, 700, 1300]
+    outs, pools = [], []
+    for fuse in (True, False):
+        bk = MI355XBackend(2, 512, 16, 8, 32, 64, device=DEV, part_pages=part_pages,
+                           fuse_append=fuse)
+        seqs, hist = _decode_batch(512, lens, 3)
+        g = torch.Generator().manual_seed(4)
+        hist = _to_dev(hist)
+        T = hist.n_tokens
+        for l in range(2):
+            bk.append_kv(l, torch.randn(T, 8, 64, generator=g).half().to(DEV),
+                         torch.randn(T, 8, 64, generator=g).half().to(DEV), hist)
+        res = []
+        for step in range(3):
+            meta = _to_dev(grow_and_assemble(seqs, [1] * len(lens), 16))
+            for l in range(2):
+                k = torch.randn(len(lens), 8, 64, generator=g).half().to(DEV)
+                v = torch.randn(len(lens), 8, 64, generator=g).half().to(DEV)
+                q = torch.randn(len(lens), 32, 64, generator=g).half().to(DEV)
+                bk.append_kv(l, k, v, meta)
+                res.append(bk.attend(q, l, 0.125, meta))
+        bk.check_device_errors()
+        outs.append(torch.stack(res))
+        pools.append(bk._pool.clone())
+    assert torch.equal(outs[0], outs[1]), "fused append changed the attention output"
+    assert torch.equal(pools[0], pools[1]), "fused append wrote different pool bytes"
+
+
+def test_deferred_append_visible_through_pool_reads():
+    print("deferred append flushed by a pool read", flush=True)
+    bk = MI355XBackend(1, 64, 16, 8, 32, 64, device=DEV)
+    seqs, hist = _decode_batch(64, [20, 5], 1)
+    meta = _to_dev(grow_and_assemble(seqs, [1, 1], 16))
+    k = torch.randn(2, 8, 64, device=DEV).half()
+    v = torch.randn(2, 8, 64, device=DEV).half()
+    bk.append_kv(0, k, v, meta)
+    assert bk._pending is not None, "decode-shaped append on the fast path should defer"
+    kf = bk.k_pool[0].view(-1, 8, 64)  # the property read lands the rows
+    vf = bk.v_pool[0].view(-1, 8, 64)
+    for t, s in enumerate(meta.slot_mapping.tolist()):
+        assert torch.equal(kf[s], k[t]) and torch.equal(vf[s], v[t])
+
+
+def test_inplace_modification_before_fused_launch_raises():
+    print("in-place modification detection", flush=True)
+    bk = MI355XBackend(1, 64, 16, 8, 32, 64, device=DEV)
+    seqs, _ = _decode_batch(64, [20], 1)
+    meta = _to_dev(grow_and_assemble(seqs, [1], 16))
+    k = torch.randn(1, 8, 64, device=DEV).half()
+    bk.append_kv(0, k, k.clone(), meta)
+    k.add_(1.0)
+    with pytest.raises(RuntimeError, match="modified in place"):
+        bk.attend(torch.randn(1, 32, 64, device=DEV).half(), 0, 0.125, meta)
+
+
+def test_fused_append_with_slot_mapping_off_the_page_table():
+    """slot_mapping naming a slot other than the page table's last position:
+    the row lands in slot_mapping's slot and attention reads the table's slot,
+    exactly as append-then-attend does in the oracle."""
+    print("fused append, slot_mapping disagreeing with the page table", flush=True)
+    p = Pair(1, 64, 16, 8, 32, 64)
+    p.poison(7)
+    seqs, hist = _decode_batch(64, [30, 40], 2)
+    check(p.step(hist, 1), "history")
+    meta = grow_and_assemble(seqs, [1, 1], 16)
+    free_page = next(b for b in range(64) if b not in meta.kv_indices.tolist())
+    odd = dataclasses.replace(meta, slot_mapping=torch.tensor(
+        [free_page * 16 + 3, int(meta.slot_mapping[1])], dtype=torch.int32))
+    res = p.step(odd, 2)
+    check(res, "off-table slot")
+    assert torch.equal(p.gpu.k_pool[0].float().cpu(), p.ref.k_pool[0]), "pool bytes differ"

@@ -46,59 +46,53 @@ def plan_decode(kv_lens, part_pages, ps=16):
     indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
     kvl = np.array(kv_lens, np.int32)
     last = np.array([k % ps or ps for k in kv_lens], np.int32)
-    cap = 8 * (int(indptr[-1]) + n) + 3 * n
+    cap = 8 * (int(indptr[-1]) + n)
     buf = np.empty(cap, np.int32)
-    nw, nsplit, ns = C.c_int32(), C.c_int32(), C.c_int32()
+    nw, ns = C.c_int32(), C.c_int32()
     rc = _native.load().pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), n, ps, part_pages,
-                                        ptr(buf), cap, C.byref(nw), C.byref(nsplit), C.byref(ns))
+                                        ptr(buf), cap, C.byref(nw), C.byref(ns))
     _native.check(rc, "plan")
-    work = buf[:8 * nw.value].reshape(-1, 8)
-    merges = buf[8 * nw.value:8 * nw.value + 3 * nsplit.value].reshape(-1, 3)
-    return indptr, npages, work, merges, ns.value
+    return indptr, npages, buf[:8 * nw.value].reshape(-1, 8), ns.value
 
 
 @pytest.mark.parametrize("part_pages", [2, 4, 8])
 def test_decode_plan_covers_every_page_once(part_pages):
+    """Every page of every sequence is in exactly one partition."""
     rng = random.Random(part_pages)
-    kv_lens = [rng.randint(1, 700) for _ in range(300)] + [16, 64, 65, 1]
-    indptr, npages, work, merges, n_slots = plan_decode(kv_lens, part_pages)
+    kv_lens = [rng.randint(1, 2048) for _ in range(300)] + [16, 64, 65, 1]
+    indptr, npages, work, n_slots = plan_decode(kv_lens, part_pages)
     covered = [[0] * p for p in npages]
     slots = []
     for seq, pbase, n, slot, kv, tok0, nparts, slot0 in work:
-        assert 1 <= n <= part_pages and kv == kv_lens[seq]
         first = pbase - indptr[seq]
-        assert tok0 == first * 16 and 0 <= first and first + n <= npages[seq]
-        assert nparts == -(-npages[seq] // part_pages)
+        assert 1 <= n <= part_pages and kv == kv_lens[seq] and tok0 == first * 16
+        assert nparts == -(-npages[seq] // part_pages) and first + n <= npages[seq]
         for p in range(first, first + n):
             covered[seq][p] += 1
         if nparts == 1:
             assert slot == -1 and slot0 == -1
         else:
-            assert slot0 <= slot < slot0 + nparts and slot - slot0 == first // part_pages
+            assert slot - slot0 == first // part_pages
             slots.append(slot)
     assert all(all(c == 1 for c in row) for row in covered)
     assert sorted(slots) == list(range(n_slots)), "partial slots must be dense and unique"
     assert list(work[:, 2]) == sorted(work[:, 2], reverse=True), "longest partitions first"
-    assert len(merges) == sum(1 for p in npages if p > part_pages)
-    for seq, s0, k in merges:
-        assert k == -(-npages[seq] // part_pages)
-        assert sorted(int(w[3]) for w in work if w[0] == seq) == list(range(s0, s0 + k))
 
 
 def test_decode_plan_rejects_inconsistent_metadata():
     lib = _native.load()
     indptr = np.array([0, 1], np.int32)
     out = np.empty(16, np.int32)
-    nw, nm, ns = C.c_int32(), C.c_int32(), C.c_int32()
+    nw, ns = C.c_int32(), C.c_int32()
     kvl = np.array([16], np.int32)
     last = np.array([9], np.int32)
     rc = lib.pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), 1, 16, 4, ptr(out), 16,
-                             C.byref(nw), C.byref(nm), C.byref(ns))
+                             C.byref(nw), C.byref(ns))
     with pytest.raises(ValueError, match="kv_last_page_len"):
         _native.check(rc, "plan")
     kvl[0] = 999
     rc = lib.pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), 1, 16, 4, ptr(out), 16,
-                             C.byref(nw), C.byref(nm), C.byref(ns))
+                             C.byref(nw), C.byref(ns))
     with pytest.raises(ValueError, match="pages supplied"):
         _native.check(rc, "plan")
 
