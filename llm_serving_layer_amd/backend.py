@@ -52,7 +52,8 @@ __all__ = ["MI355XBackend", "is_available", "unavailable_reason"]
 _DTYPES = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16,
            torch.float32: _native.DTYPE_F32}
 
-DEFAULT_PART_PAGES = 4   # split-K partition: 4 pages = 64 tokens per wave
+DEFAULT_PART_PAGES = 8   # split-K partition: 8 pages = 128 tokens per wave
+MAX_PART_PAGES = 64      # a partition's page ids are read by one wavefront
 DEFAULT_Q_TILE = 64
 
 
@@ -73,7 +74,7 @@ class _Plan:
     """Device-side metadata and launch plan for one BatchMeta (one step)."""
 
     __slots__ = ("meta", "use_prefill", "slots", "indptr", "indices", "kv_lens", "cu_q",
-                 "bidx", "plan", "n_work", "n_slots", "n_tokens", "n_seqs")
+                 "bidx", "plan", "n_work", "n_slots", "n_tokens", "n_seqs", "fusable")
 
 
 class _Pending:
@@ -105,6 +106,8 @@ class MI355XBackend:
                              f"got {dtype}")
         if head_dim > 256:
             raise ValueError(f"head_dim={head_dim} > 256 is not supported")
+        if not 1 <= part_pages <= MAX_PART_PAGES:
+            raise ValueError(f"part_pages={part_pages} must be in [1, {MAX_PART_PAGES}]")
         try:
             self._lib = _native.load()
         except RuntimeError as exc:
@@ -276,7 +279,7 @@ class MI355XBackend:
                 p = self._ensure_planned(meta)
             except ValueError:
                 p = None  # inconsistent paging metadata: append now, attend will raise
-            if p is not None and not p.use_prefill:
+            if p is not None and p.fusable:
                 pend = _Pending()
                 pend.layer, pend.k, pend.v, pend.meta = layer_idx, k, v, meta
                 pend.slots, pend.stream = p.slots, stream
@@ -342,7 +345,7 @@ class MI355XBackend:
         stream = _current_stream(self.device)
         pend = self._pending
         fused = (pend is not None and pend.layer == layer_idx and pend.meta is meta
-                 and pend.stream == stream and not p.use_prefill)
+                 and pend.stream == stream and p.fusable)
         if fused:
             self._check_pending_intact(pend)
             self._pending = None
@@ -388,15 +391,20 @@ class MI355XBackend:
         if pl is not None and pl.meta is meta:
             return pl
         n = meta.n_seqs
+        parts = [meta.query_lens, meta.cu_query_lens, meta.kv_lens, meta.kv_indptr,
+                 meta.kv_last_page_len]
+        # For the fused append: each sequence's last page id and its new slot.
+        with_slots = (meta.slot_mapping is not None and meta.slot_mapping.shape[0] == n
+                      and meta.kv_indices.shape[0] > 0 and meta.kv_indptr.shape[0] == n + 1)
+        if with_slots:
+            last_ix = (meta.kv_indptr[1:].to(torch.int64) - 1).clamp(
+                0, meta.kv_indices.shape[0] - 1)
+            parts += [meta.kv_indices[last_ix], meta.slot_mapping]
         # ONE device->host transfer for everything the host plan reads.
-        host = torch.cat([meta.query_lens.reshape(-1).to(torch.int64),
-                          meta.cu_query_lens.reshape(-1).to(torch.int64),
-                          meta.kv_lens.reshape(-1).to(torch.int64),
-                          meta.kv_indptr.reshape(-1).to(torch.int64),
-                          meta.kv_last_page_len.reshape(-1).to(torch.int64)]).cpu().numpy()
+        host = torch.cat([t.reshape(-1).to(torch.int64) for t in parts]).cpu().numpy()
         ql, cu = host[:n], host[n:2 * n + 1]
         kvl, indptr = host[2 * n + 1:3 * n + 1], host[3 * n + 1:4 * n + 2]
-        last = host[4 * n + 2:]
+        last = host[4 * n + 2:5 * n + 2]
         use_prefill = bool((ql > 1).any())
         if bool(meta.is_prefill) != use_prefill:
             raise ValueError(
@@ -406,6 +414,13 @@ class MI355XBackend:
             )
         p = _Plan()
         p.meta, p.use_prefill = meta, use_prefill
+        # Fusing the append into attention is exact only if every sequence's
+        # new row lands at the last slot of its own page list (then no other
+        # sequence of the launch reads that slot).
+        p.fusable = False
+        if with_slots and not use_prefill:
+            last_page, new_slot = host[5 * n + 2:6 * n + 2], host[6 * n + 2:7 * n + 2]
+            p.fusable = bool((new_slot == last_page * self.block_size + last - 1).all())
         p.n_seqs, p.n_tokens = n, int(cu[-1])
         if p.n_tokens != meta.n_tokens:
             raise ValueError(f"cu_query_lens ends at {p.n_tokens} but meta has "

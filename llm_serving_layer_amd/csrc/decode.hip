@@ -1,46 +1,47 @@
 // Paged decode attention for gfx950 (every sequence has one query token).
 //
 // Work decomposition (planned on the host once per batch): a sequence's
-// pages are cut into partitions of at most PP pages (split-K over the KV
-// axis; the split depends only on that sequence's own length, so its result
-// never depends on what it is batched with). A workgroup owns one partition
-// and its waves own one KV head each, so they request the same pages
-// together (the heads of a token row are adjacent in memory). One partition
-// per wave, no loop and no barrier: the kernel keeps 5 waves per SIMD.
+// pages are cut into partitions of at most part_pages pages (split-K over
+// the KV axis; the split depends only on that sequence's own length, so its
+// result never depends on what it is batched with). A workgroup owns one
+// partition and its waves own one KV head each, so they request the same
+// pages together (the heads of a token row are adjacent in memory).
 //
-// Per wave and partition (G query heads share the KV head, G <= 16):
-//  1. one wave-wide load of the partition's page ids, broadcast by readlane;
-//     every K and V load of the partition is issued before any arithmetic;
-//  2. S^T = K Q^T with one 16x16x32 MFMA per 32 dims of a 16-token page: the
+// A wave walks its partition GP pages at a time with an online softmax, and
+// the next GP pages are always in flight while the current ones are used:
+// the K registers are refilled as soon as S is computed, the V registers as
+// soon as V has been copied to LDS. Per GP pages (G query heads share the KV
+// head, G <= 16):
+//  1. S^T = K Q^T with one 16x16x32 MFMA per 32 dims of a 16-token page: the
 //     K rows ARE the A operand (lane (token m, group g) holds 16 contiguous
 //     bytes of row m), Q^T the B operand (column n = query head n, zero
 //     beyond G). Lane (head n, group g) then holds the scores of tokens
 //     4g..4g+3 of the page for head n;
-//  3. softmax in registers: mask past kv_len, running max / sum over the
-//     wave's partitions with one in-lane pass plus two cross-lane steps;
-//     p = 2^(s*scale*log2e - m) rounded to the pool dtype -- four values per
-//     lane that are exactly the A operand of a 16x16x16 MFMA;
-//  4. PV on MFMA: the V page goes to LDS row-major and ds_read_b64_tr_b16
+//  2. softmax in registers: mask past kv_len, running max / sum with one
+//     in-lane pass plus two cross-lane steps; p = 2^(s*scale*log2e - m)
+//     rounded to the pool dtype -- four values per lane that are exactly the
+//     A operand of a 16x16x16 MFMA;
+//  3. PV on MFMA: the V pages go to LDS row-major and ds_read_b64_tr_b16
 //     hands each lane 4 consecutive tokens of one dim, the B operand, one
 //     read per 16 dims. Tokens past kv_len are zeroed so stale bits can
 //     never reach the sum.
 //
 // Split sequences merge in the same launch. Each partition publishes its
-// partial (o, m, l) with agent-scope stores, which write through the
-// per-XCD L2 to the memory-side coherence point, waits until they have
+// partial (o, m, l) with 16-byte buffer stores carrying the sc1 (agent
+// coherence) bit, which write through the per-XCD L2, waits until they have
 // completed (s_waitcnt vmcnt(0)), then bumps an arrival counter for its
 // (sequence, KV head). The wave that sees the last arrival reads the
-// partials back with agent-scope loads (which do not hit a stale L2 line)
-// and writes the output. This avoids a second launch and also avoids an
-// agent-scope release fence, whose L2 write-back walks the whole cache and
-// measured ~10x slower per wave than the merge itself.
+// partials back with sc1 loads (never a stale L2 line) and writes the
+// output. This avoids a second launch and an agent-scope release fence,
+// whose L2 write-back walks the whole cache.
 //
 // Fused append (optional): when the caller passes the step's new K/V rows,
 // the wave that owns a sequence's last page writes the row of its head to
-// slot_mapping's slot and patches the copy it already loaded, so a decode
-// step costs one launch per layer instead of two. The patch is applied only
-// when slot_mapping names the same slot as the page table, so the result is
-// exactly "append, then attend".
+// slot_mapping's slot and patches the copy it loaded, so a decode step costs
+// one launch per layer instead of two. The patch is applied only when
+// slot_mapping names the same slot as the page table, so the result is
+// exactly "append, then attend" (the caller guarantees that no other
+// sequence of the launch reads that slot).
 #include <algorithm>
 #include <vector>
 
@@ -52,11 +53,15 @@ namespace pkv {
 //  slot (-1: the partition is the whole sequence), kv_len, first token,
 //  n_partitions of the sequence, first slot of the sequence}
 constexpr int kWorkInts = 8;
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;         // KV heads (waves) per workgroup, at most
+constexpr int kMaxPartPages = 64; // a partition's page ids fit one wave-wide load
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 template <typename T> struct Mma;
@@ -91,23 +96,44 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <typename T, int D, int G, int PP>
+// Buffer resource over the split-K workspace: raw (untyped) 32-bit records,
+// hardware range check against `bytes` (out-of-range loads read 0, stores
+// are dropped). kSc1 on a load/store = agent-scope coherent access.
+constexpr int kSc1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
+}
+
+// Layout of one partition's partial output: per (slot, KV head), NGR groups
+// of 4 head rows, each NDB dim blocks of 16 lanes x 4 rows (float4 per
+// lane) -- exactly the MFMA accumulator layout, so a wave stores and loads
+// it with one 16-byte access per lane and dim block.
+template <int D, int G> struct PartLayout {
+  static constexpr int NGR = (G + 3) / 4;
+  static constexpr int NDB = D / 16;
+  static constexpr int FLOATS = NGR * NDB * 64;  // per (slot, KV head)
+};
+
+template <typename T, int D, int G>
 __global__ __launch_bounds__(kWaves * 64) void decode_kernel(
     const T* __restrict__ q, T* __restrict__ out, T* __restrict__ kpool, T* __restrict__ vpool,
     int64_t num_blocks, const int32_t* __restrict__ kv_indices,
     const int32_t* __restrict__ work, int32_t n_kv_heads, float scale_log2,
     const T* __restrict__ k_new, const T* __restrict__ v_new,
     const int32_t* __restrict__ slot_mapping, float* part_o, float* part_ml,
-    int32_t* counters, int32_t* status) {
+    uint32_t o_bytes, uint32_t ml_bytes, int32_t* counters, int32_t* status) {
   typedef typename Mma<T>::vec8 vec8;
   typedef typename Mma<T>::vec4 vec4;
+  typedef PartLayout<D, G> PL;
   constexpr int PS = 16;
-  constexpr int NCH = D / 32;   // QK MFMA k-chunks per page
-  constexpr int NDB = D / 16;   // PV MFMA dim blocks
-  constexpr int VL = D / 8;     // lanes per V row when loading (16 bytes each)
-  constexpr int VROWS = 64 / VL;          // V rows per load instruction
-  constexpr int VLOADS = PS / VROWS;      // load instructions per V page
-  constexpr int TILE = PP * PS * D;       // V tile elements per wave
+  constexpr int GP = D <= 64 ? 4 : 2;   // pages per register tile
+  constexpr int NCH = D / 32;           // QK MFMA k-chunks per page
+  constexpr int NDB = D / 16;           // PV MFMA dim blocks
+  constexpr int VL = D / 8;             // lanes per V row when loading (16 bytes each)
+  constexpr int VROWS = 64 / VL;        // V rows per load instruction
+  constexpr int VLOADS = PS / VROWS;    // load instructions per V page
+  constexpr int TILE = GP * PS * D;     // V tile elements per wave
+  constexpr int NGR = PL::NGR;
 
   extern __shared__ __align__(16) unsigned char smem[];
   const int wave = threadIdx.x >> 6;
@@ -127,11 +153,52 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(
   const int g = lane >> 4;   // MFMA k-group
   const int vr_ = lane / VL, vc_ = lane % VL;
 
+  // Lane j holds the partition's j-th page id (npp <= 64).
   int pid = 0;
   if (lane < npp) pid = kv_indices[pbase + lane];
   const bool bad = lane < npp && (pid < 0 || (int64_t)pid >= num_blocks);
   if (bad) pid = 0;
   if (__builtin_amdgcn_ballot_w64(bad) && lane == 0) flag(status, PKV_STATUS_BAD_PAGE);
+
+  // K/V loads go through a buffer resource per page: the page base is
+  // wave-uniform (scalar registers) and every lane's offset within a page is
+  // the same for all pages, so an address costs one VGPR, not two per load.
+  // The resource's range is the page itself; nt: the pages are streamed once.
+  const uint32_t page_bytes = (uint32_t)(PS * row * (int64_t)sizeof(T));
+  const uint32_t koff = (uint32_t)((n * row + (int64_t)h * D + g * 8) * sizeof(T));
+  const uint32_t voff = (uint32_t)((vr_ * row + (int64_t)h * D + vc_ * 8) * sizeof(T));
+  const uint32_t vstep = (uint32_t)(VROWS * row * sizeof(T));
+  constexpr int kNt = 2;
+  vec8 kt[GP][NCH];
+  vec8 vt[GP][VLOADS];
+  auto load_k = [&](int p0) {
+#pragma unroll
+    for (int j = 0; j < GP; ++j) {
+      if (p0 + j < npp) {
+        const int64_t page = __builtin_amdgcn_readlane(pid, p0 + j);
+        const __amdgpu_buffer_rsrc_t rk = ws_rsrc(kpool + page * PS * row, page_bytes);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+          kt[j][c] = __builtin_bit_cast(
+              vec8, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + c * 32 * sizeof(T), 0, kNt));
+      }
+    }
+  };
+  auto load_v = [&](int p0) {
+#pragma unroll
+    for (int j = 0; j < GP; ++j) {
+      if (p0 + j < npp) {
+        const int64_t page = __builtin_amdgcn_readlane(pid, p0 + j);
+        const __amdgpu_buffer_rsrc_t rv = ws_rsrc(vpool + page * PS * row, page_bytes);
+#pragma unroll
+        for (int u = 0; u < VLOADS; ++u)
+          vt[j][u] = __builtin_bit_cast(
+              vec8, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, u * vstep, kNt));
+      }
+    }
+  };
+  load_k(0);
+  load_v(0);
 
   // Q^T as the QK B operand: column n = query head h*G + n (zero beyond G).
   vec8 qb[NCH];
@@ -144,120 +211,138 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(
     }
   }
 
-  // Issue every K and V load of the partition.
-  vec8 kt[PP][NCH];
-  vec8 vt[PP][VLOADS];
-#pragma unroll
-  for (int j = 0; j < PP; ++j) {
-    if (j < npp) {
-      const int64_t page = __builtin_amdgcn_readlane(pid, j);
-      const T* kr = kpool + (page * PS + n) * row + (int64_t)h * D + g * 8;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) kt[j][c] = *reinterpret_cast<const vec8*>(kr + c * 32);
-#pragma unroll
-      for (int u = 0; u < VLOADS; ++u)
-        vt[j][u] = *reinterpret_cast<const vec8*>(vpool + (page * PS + u * VROWS + vr_) * row +
-                                                  (int64_t)h * D + vc_ * 8);
-    }
-  }
-
-  if (k_new && tok0 + npp * PS >= kv_len) {
-    // This wave owns the sequence's newest token for head h.
-    const int jl = npp - 1;
-    const int tl = (kv_len - 1) % PS;
-    const int64_t csr_slot = (int64_t)__builtin_amdgcn_readlane(pid, jl) * PS + tl;
+  // Fused append: the wave whose partition holds the newest token writes its
+  // head's row now; the loaded copy is patched when its page is used.
+  const bool owns_last = k_new != nullptr && tok0 + npp * PS >= kv_len;
+  const int tl = (kv_len - 1) % PS;   // newest token's row within its page
+  bool patch = false;
+  if (owns_last) {
+    const int64_t csr_slot = (int64_t)__builtin_amdgcn_readlane(pid, npp - 1) * PS + tl;
     const int64_t new_slot = slot_mapping[seq];
     const bool in_range = new_slot >= 0 && new_slot < num_blocks * PS;
     if (!in_range && lane == 0) flag(status, PKV_STATUS_BAD_SLOT);
-    const bool patch = new_slot == csr_slot;
-    const T* kn = k_new + ((int64_t)seq * n_kv_heads + h) * D;
-    const T* vn = v_new + ((int64_t)seq * n_kv_heads + h) * D;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (n == tl) {
-        const vec8 x = *reinterpret_cast<const vec8*>(kn + c * 32 + g * 8);
-        if (in_range)
-          *reinterpret_cast<vec8*>(kpool + new_slot * row + (int64_t)h * D + c * 32 + g * 8) = x;
-#pragma unroll
-        for (int j = 0; j < PP; ++j)  // static indices keep kt in registers
-          if (patch && j == jl) kt[j][c] = x;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < VLOADS; ++u) {
-      if (u * VROWS + vr_ == tl) {
-        const vec8 x = *reinterpret_cast<const vec8*>(vn + vc_ * 8);
-        if (in_range)
-          *reinterpret_cast<vec8*>(vpool + new_slot * row + (int64_t)h * D + vc_ * 8) = x;
-#pragma unroll
-        for (int j = 0; j < PP; ++j)
-          if (patch && j == jl) vt[j][u] = x;
+    patch = new_slot == csr_slot;
+    if (in_range) {
+      const T* kn = k_new + ((int64_t)seq * n_kv_heads + h) * D;
+      const T* vn = v_new + ((int64_t)seq * n_kv_heads + h) * D;
+      if (lane < VL) {
+        *reinterpret_cast<vec8*>(kpool + new_slot * row + (int64_t)h * D + lane * 8) =
+            *reinterpret_cast<const vec8*>(kn + lane * 8);
+        *reinterpret_cast<vec8*>(vpool + new_slot * row + (int64_t)h * D + lane * 8) =
+            *reinterpret_cast<const vec8*>(vn + lane * 8);
       }
     }
   }
 
-  // V pages into this wave's LDS tile, row-major [token][dim]; rows past
-  // kv_len are zeroed.
-#pragma unroll
-  for (int j = 0; j < PP; ++j) {
-    if (j < npp) {
-#pragma unroll
-      for (int u = 0; u < VLOADS; ++u) {
-        const int t = u * VROWS + vr_;
-        vec8 x = vt[j][u];
-        if (tok0 + j * PS + t >= kv_len) x = vec8{};
-        *reinterpret_cast<vec8*>(vlds + (j * PS + t) * D + vc_ * 8) = x;
-      }
-    }
-  }
-
-  // S^T per page; lane (n, g) holds tokens 4g..4g+3 of page j for head n.
-  float s[PP][4];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < PP; ++j) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (j < npp) {
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) acc = Mma<T>::qk(kt[j][c], qb[c], acc);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool live = j < npp && tok0 + j * PS + 4 * g + i < kv_len;
-      s[j][i] = live ? acc[i] * scale_log2 : -INFINITY;
-      mx = fmaxf(mx, s[j][i]);
-    }
-  }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-
-  vec4 p[PP];
-  float lsum = 0.f;
-#pragma unroll
-  for (int j = 0; j < PP; ++j) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float e = __builtin_amdgcn_exp2f(s[j][i] - mx);
-      lsum += e;
-      p[j][i] = (T)e;
-    }
-  }
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
-  wave_lds_sync();
-
-  // O (rows = heads, cols = dims) += P V; B operand by transposing reads.
+  const int ng = (npp + GP - 1) / GP;
   f32x4 o[NDB];
 #pragma unroll
   for (int b = 0; b < NDB; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;  // per head n (replicated over g)
+
+  for (int gi = 0; gi < ng; ++gi) {
+    const int p0 = gi * GP;
+    if (patch && gi == ng - 1) {
+      const int jj = npp - 1 - p0;  // the newest page within this tile
+      const T* kn = k_new + ((int64_t)seq * n_kv_heads + h) * D;
+      const T* vn = v_new + ((int64_t)seq * n_kv_heads + h) * D;
 #pragma unroll
-  for (int j = 0; j < PP; ++j) {
-    if (j < npp) {
-      const T* base = vlds + (j * PS + 4 * g + (n >> 2)) * D + 4 * (n & 3);
+      for (int c = 0; c < NCH; ++c) {
+        if (n == tl) {
+          const vec8 x = *reinterpret_cast<const vec8*>(kn + c * 32 + g * 8);
 #pragma unroll
-      for (int b = 0; b < NDB; ++b) {
-        const i16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + 16 * b));
-        o[b] = Mma<T>::pv(p[j], __builtin_bit_cast(vec4, raw), o[b]);
+          for (int j = 0; j < GP; ++j)  // static indices keep kt in registers
+            if (j == jj) kt[j][c] = x;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < VLOADS; ++u) {
+        if (u * VROWS + vr_ == tl) {
+          const vec8 x = *reinterpret_cast<const vec8*>(vn + vc_ * 8);
+#pragma unroll
+          for (int j = 0; j < GP; ++j)
+            if (j == jj) vt[j][u] = x;
+        }
+      }
+    }
+
+    // S^T per page; lane (n, g) holds tokens 4g..4g+3 of page j for head n.
+    float s[GP][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < GP; ++j) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (p0 + j < npp) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) acc = Mma<T>::qk(kt[j][c], qb[c], acc);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool live = p0 + j < npp && tok0 + (p0 + j) * PS + 4 * g + i < kv_len;
+        s[j][i] = live ? acc[i] * scale_log2 : -INFINITY;
+        mx = fmaxf(mx, s[j][i]);
+      }
+    }
+    if (gi + 1 < ng) load_k(p0 + GP);  // K registers are free again
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);  // finite: every tile has a live token
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+
+    vec4 p[GP];
+    float ls = 0.f;
+#pragma unroll
+    for (int j = 0; j < GP; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f(s[j][i] - m_new);
+        ls += e;
+        p[j][i] = (T)e;
+      }
+    }
+    ls += __shfl_xor(ls, 16, 64);
+    ls += __shfl_xor(ls, 32, 64);
+    l_run = l_run * alpha + ls;
+    m_run = m_new;
+
+    // V pages into this wave's LDS tile, row-major [token][dim]; rows past
+    // kv_len are zeroed. The previous tile's transposing reads are done.
+    wave_lds_sync();
+#pragma unroll
+    for (int j = 0; j < GP; ++j) {
+      if (p0 + j < npp) {
+#pragma unroll
+        for (int u = 0; u < VLOADS; ++u) {
+          const int t = u * VROWS + vr_;
+          vec8 x = vt[j][u];
+          if (tok0 + (p0 + j) * PS + t >= kv_len) x = vec8{};
+          *reinterpret_cast<vec8*>(vlds + (j * PS + t) * D + vc_ * 8) = x;
+        }
+      }
+    }
+    if (gi + 1 < ng) load_v(p0 + GP);  // V registers are free again
+
+    // Rescale O: lane (n, g) holds head rows 4g+i, whose factor lives in lane 4g+i.
+    if (gi > 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+        for (int b = 0; b < NDB; ++b) o[b][i] *= a;
+      }
+    }
+    wave_lds_sync();
+
+    // O (rows = heads, cols = dims) += P V; B operand by transposing reads.
+#pragma unroll
+    for (int j = 0; j < GP; ++j) {
+      if (p0 + j < npp) {
+        const T* base = vlds + (j * PS + 4 * g + (n >> 2)) * D + 4 * (n & 3);
+#pragma unroll
+        for (int b = 0; b < NDB; ++b) {
+          const i16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + 16 * b));
+          o[b] = Mma<T>::pv(p[j], __builtin_bit_cast(vec4, raw), o[b]);
+        }
       }
     }
   }
@@ -267,7 +352,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * g + i;
-      const float li = __shfl(lsum, r, 64);  // lane r holds head r's sum
+      const float li = __shfl(l_run, r, 64);  // lane r holds head r's sum
       if (r < G) {
 #pragma unroll
         for (int b = 0; b < NDB; ++b)
@@ -278,20 +363,19 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(
   }
 
   // ---- split sequence: publish, count, and the last arrival merges --------
+  const __amdgpu_buffer_rsrc_t ro = ws_rsrc(part_o, o_bytes);
+  const uint32_t head_off = (uint32_t)(((int64_t)slot * n_kv_heads + h) * PL::FLOATS * 4);
+  if (g < NGR) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 4 * g + i;
-    if (r < G) {
-#pragma unroll
-      for (int b = 0; b < NDB; ++b)
-        __hip_atomic_store(part_o + ((int64_t)slot * Hq + h * G + r) * D + 16 * b + n,
-                           o[b][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    for (int b = 0; b < NDB; ++b)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[b]), ro,
+                                             head_off + ((g * NDB + b) * 16 + n) * 16, 0, kSc1);
   }
   if (lane < G) {
-    float* pm = part_ml + ((int64_t)slot * Hq + h * G + lane) * 2;
-    __hip_atomic_store(pm, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(pm + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const __amdgpu_buffer_rsrc_t rm = ws_rsrc(part_ml, ml_bytes);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l_run}), rm,
+                                          (uint32_t)(((int64_t)slot * Hq + h * G + lane) * 8),
+                                          0, kSc1);
   }
   // Every partial store of this wave has completed at the coherence point
   // before the arrival is counted.
@@ -302,21 +386,27 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(
   old = __builtin_amdgcn_readfirstlane(old);
   if (old != nparts - 1) return;
 
-  // Last arrival for (seq, h). Lanes run over partitions to get each head
-  // row's max M and sum L, then, 64 partitions at a time, put the weights
-  // 2^(m_s - M) in this wave's (now free) LDS tile and read the partial
-  // outputs in batches of MB partitions with all of a lane's values at once:
-  // a long sequence costs a few dependent round trips, not one per partition.
-  float* wts = reinterpret_cast<float*>(vlds);  // [64][G]; the tile holds >= 64*G floats
+  // Last arrival for (seq, h). Lanes run over partitions for each head
+  // row's max M and sum L; then, 64 partitions at a time, the weights
+  // 2^(m_s - M) go to this wave's (now free) LDS tile as [partition][16
+  // rows], and the partial outputs are read in the producers' own layout:
+  // lane (n, g) takes row group rg = g % NGR of every SPLIT-th partition
+  // starting at g / NGR, MB partitions per round trip, and the SPLIT lane
+  // groups that share a row group are summed by shuffles at the end.
+  constexpr int SPLIT = 4 / NGR;
+  constexpr int MB = NDB >= 8 ? 2 : 4;
+  const int rg = g % NGR, so = g / NGR;
+  float* wts = reinterpret_cast<float*>(vlds);  // [64][16]; the tile holds >= 1024 floats
+  const __amdgpu_buffer_rsrc_t rm = ws_rsrc(part_ml, ml_bytes);
   auto load_ml = [&](int c0, float* mr, float* lr) {
     const bool ok = c0 + lane < nparts;
-    const int64_t b2 = ((int64_t)(slot0 + (ok ? c0 + lane : 0)) * Hq + h * G) * 2;
+    const uint32_t b2 = (uint32_t)(((int64_t)(slot0 + (ok ? c0 + lane : 0)) * Hq + h * G) * 8);
 #pragma unroll
     for (int r = 0; r < G; ++r) {
-      mr[r] = ok ? __hip_atomic_load(part_ml + b2 + 2 * r, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
-      lr[r] = ok ? __hip_atomic_load(part_ml + b2 + 2 * r + 1, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+      const f32x2 ml =
+          __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rm, b2 + 8 * r, 0, kSc1));
+      mr[r] = ok ? ml[0] : -INFINITY;
+      lr[r] = ok ? ml[1] : 0.f;
     }
   };
   float mr[G], lr[G], M[G], L[G];
@@ -327,57 +417,71 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(
 #pragma unroll
     for (int r = 0; r < G; ++r) M[r] = fmaxf(M[r], wave_max(mr[r]));
   }
-  constexpr int VALS = (G * D + 63) / 64;
-  constexpr int MB = VALS >= 16 ? 1 : 16 / VALS;  // partitions per load batch
-  float acc[VALS];
+  f32x4 acc[NDB];
 #pragma unroll
-  for (int i = 0; i < VALS; ++i) acc[i] = 0.f;
+  for (int b = 0; b < NDB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int c0 = 0; c0 < nparts; c0 += 64) {
     if (nparts > 64) load_ml(c0, mr, lr);  // else still in registers
+    f32x4 wv4[4];
 #pragma unroll
-    for (int r = 0; r < G; ++r) {
-      const float wv = c0 + lane < nparts ? __builtin_amdgcn_exp2f(mr[r] - M[r]) : 0.f;
-      L[r] += wave_sum(wv * lr[r]);
-      wts[lane * G + r] = wv;
+    for (int r = 0; r < 16; ++r) {
+      float wv = 0.f;
+      if (r < G) {
+        wv = c0 + lane < nparts ? __builtin_amdgcn_exp2f(mr[r] - M[r]) : 0.f;
+        L[r] += wave_sum(wv * lr[r]);
+      }
+      wv4[r / 4][r % 4] = wv;
     }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) *reinterpret_cast<f32x4*>(wts + lane * 16 + 4 * k) = wv4[k];
     wave_lds_sync();
     const int cn = min(64, nparts - c0);
-    for (int s0 = 0; s0 < cn; s0 += MB) {
-      float v[MB][VALS];
+    for (int s0 = so; s0 < cn; s0 += SPLIT * MB) {
+      f32x4 v[MB][NDB];
 #pragma unroll
       for (int u = 0; u < MB; ++u) {
-        const bool ok = s0 + u < cn;
-        const float* po = part_o + ((int64_t)(slot0 + c0 + (ok ? s0 + u : 0)) * Hq + h * G) * D;
+        const int sl = s0 + u * SPLIT;
+        const uint32_t off = (uint32_t)(((int64_t)(slot0 + c0 + (sl < cn ? sl : 0)) * n_kv_heads + h) *
+                                        PL::FLOATS * 4);
 #pragma unroll
-        for (int i = 0; i < VALS; ++i) {
-          const int idx = lane + 64 * i;
-          v[u][i] = (ok && idx < G * D)
-                        ? __hip_atomic_load(po + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                        : 0.f;
-        }
+        for (int b = 0; b < NDB; ++b)
+          v[u][b] = sl < cn ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                  ro, off + ((rg * NDB + b) * 16 + n) * 16, 0, kSc1))
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
       for (int u = 0; u < MB; ++u) {
-        if (s0 + u >= cn) break;
+        const int sl = s0 + u * SPLIT;
+        if (sl < cn) {
+          const f32x4 wr = *reinterpret_cast<const f32x4*>(wts + sl * 16 + 4 * rg);
 #pragma unroll
-        for (int i = 0; i < VALS; ++i) {
-          const int idx = lane + 64 * i;
-          if (idx < G * D) acc[i] += wts[(s0 + u) * G + idx / D] * v[u][i];
+          for (int b = 0; b < NDB; ++b) acc[b] += wr * v[u][b];
         }
       }
     }
     wave_lds_sync();  // the next chunk rewrites the weights
   }
 #pragma unroll
-  for (int i = 0; i < VALS; ++i) {
-    const int idx = lane + 64 * i;
-    if (idx < G * D) {
-      const int r = idx / D;
+  for (int b = 0; b < NDB; ++b) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (SPLIT >= 4) acc[b][i] += __shfl_xor(acc[b][i], 16, 64);
+      if (SPLIT >= 2) acc[b][i] += __shfl_xor(acc[b][i], 32, 64);
+    }
+  }
+  if (so == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * rg + i;
       float lr_ = L[0];
 #pragma unroll
       for (int rr = 1; rr < G; ++rr)  // static indices keep L in registers
         if (r == rr) lr_ = L[rr];
-      out[((int64_t)seq * Hq + h * G) * D + idx] = (T)(acc[i] / lr_);
+      if (r < G) {
+#pragma unroll
+        for (int b = 0; b < NDB; ++b)
+          out[((int64_t)seq * Hq + h * G + r) * D + 16 * b + n] = (T)(acc[b][i] / lr_);
+      }
     }
   }
   if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -389,59 +493,57 @@ static int heads_per_workgroup(int Hkv) {
   return 1;
 }
 
-template <typename T, int D, int G, int PP>
+template <typename T, int D, int G>
 static void launch(const void* q, void* out, void* kp, void* vp, int64_t nb,
                    const int32_t* indices, const int32_t* work, int32_t n_work, int32_t Hkv,
                    float sl2, const void* kn, const void* vn, const int32_t* slots, float* po,
-                   float* pml, int32_t* cnt, int32_t* status, hipStream_t s) {
+                   float* pml, uint32_t o_bytes, uint32_t ml_bytes, int32_t* cnt,
+                   int32_t* status, hipStream_t s) {
+  constexpr int GP = D <= 64 ? 4 : 2;
   const int hw = heads_per_workgroup(Hkv);
-  const size_t lds = (size_t)hw * PP * 16 * D * sizeof(T);
-  hipLaunchKernelGGL((decode_kernel<T, D, G, PP>), dim3((unsigned)(n_work * (Hkv / hw))),
+  const size_t lds = (size_t)hw * GP * 16 * D * sizeof(T);
+  hipLaunchKernelGGL((decode_kernel<T, D, G>), dim3((unsigned)(n_work * (Hkv / hw))),
                      dim3(hw * 64), lds, s, (const T*)q, (T*)out, (T*)kp, (T*)vp, nb, indices,
-                     work, Hkv, sl2, (const T*)kn, (const T*)vn, slots, po, pml, cnt, status);
+                     work, Hkv, sl2, (const T*)kn, (const T*)vn, slots, po, pml, o_bytes,
+                     ml_bytes, cnt, status);
 }
 
 typedef void (*LaunchFn)(const void*, void*, void*, void*, int64_t, const int32_t*,
                          const int32_t*, int32_t, int32_t, float, const void*, const void*,
-                         const int32_t*, float*, float*, int32_t*, int32_t*, hipStream_t);
-
-template <typename T, int D, int G>
-static LaunchFn pick_pp(int pp) {
-  switch (pp) {
-    case 2: return launch<T, D, G, 2>;
-    case 4: return launch<T, D, G, 4>;
-    case 8: return launch<T, D, G, 8>;
-    default: return nullptr;
-  }
-}
+                         const int32_t*, float*, float*, uint32_t, uint32_t, int32_t*,
+                         int32_t*, hipStream_t);
 
 template <typename T, int D>
-static LaunchFn pick_g(int G, int pp) {
+static LaunchFn pick_g(int G) {
   switch (G) {
-    case 1: return pick_pp<T, D, 1>(pp);
-    case 2: return pick_pp<T, D, 2>(pp);
-    case 4: return pick_pp<T, D, 4>(pp);
-    case 8: return pick_pp<T, D, 8>(pp);
-    case 16: return pick_pp<T, D, 16>(pp);
+    case 1: return launch<T, D, 1>;
+    case 2: return launch<T, D, 2>;
+    case 4: return launch<T, D, 4>;
+    case 8: return launch<T, D, 8>;
+    case 16: return launch<T, D, 16>;
     default: return nullptr;
   }
 }
 
 template <typename T>
-static LaunchFn pick(int D, int G, int pp) {
+static LaunchFn pick(int D, int G) {
   switch (D) {
-    case 64: return pick_g<T, 64>(G, pp);
-    case 128: return pp <= 4 ? pick_g<T, 128>(G, pp) : nullptr;
+    case 64: return pick_g<T, 64>(G);
+    case 128: return pick_g<T, 128>(G);
     default: return nullptr;
   }
 }
 
 static LaunchFn fast_decode(int32_t dtype, int32_t D, int32_t G, int32_t page_size, int32_t pp) {
-  if (page_size != 16) return nullptr;
-  if (dtype == PKV_DTYPE_F16) return pick<_Float16>(D, G, pp);
-  if (dtype == PKV_DTYPE_BF16) return pick<__bf16>(D, G, pp);
+  if (page_size != 16 || pp < 1 || pp > kMaxPartPages) return nullptr;
+  if (dtype == PKV_DTYPE_F16) return pick<_Float16>(D, G);
+  if (dtype == PKV_DTYPE_BF16) return pick<__bf16>(D, G);
   return nullptr;
 }
+
+// Floats of partial output per (slot, KV head): the accumulator tile of
+// ceil(G/4) groups of 4 head rows.
+static int64_t part_floats(int32_t G, int32_t D) { return (int64_t)((G + 3) / 4) * 4 * D; }
 
 // generic fallback lives in attention.hip
 int generic_decode(const void* q, void* out, const void* kp, const void* vp, int64_t nb,
@@ -466,8 +568,9 @@ extern "C" int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_lens,
                                int32_t page_size, int32_t part_pages, int32_t* plan,
                                int64_t plan_capacity, int32_t* n_work_out,
                                int32_t* n_slots_out) {
-  if (n_seqs <= 0 || page_size <= 0 || part_pages <= 0)
-    return fail(PKV_ERR_INVALID, "n_seqs, page_size and part_pages must be positive");
+  if (n_seqs <= 0 || page_size <= 0 || part_pages <= 0 || part_pages > kMaxPartPages)
+    return fail(PKV_ERR_INVALID, "n_seqs and page_size must be positive and part_pages in "
+                "[1, %d]", kMaxPartPages);
   if (kv_indptr[0] != 0) return fail(PKV_ERR_INVALID, "kv_indptr must start at 0");
   struct Item { int32_t v[kWorkInts]; };
   std::vector<Item> items;
@@ -487,9 +590,11 @@ extern "C" int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_lens,
     }
     if (parts > 1) slots += parts;
   }
-  // Longest partitions first, so the short tail items fill in behind them.
-  std::stable_sort(items.begin(), items.end(),
-                   [](const Item& a, const Item& b) { return a.v[2] > b.v[2]; });
+  // Longest partitions first, so the short tail items fill in behind them;
+  // among equals, longer sequences first so their merges start early.
+  std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) {
+    return a.v[2] != b.v[2] ? a.v[2] > b.v[2] : a.v[4] > b.v[4];
+  });
   const int64_t need = (int64_t)kWorkInts * items.size();
   if (need > plan_capacity)
     return fail(PKV_ERR_CAPACITY, "plan needs %lld entries, capacity %lld", (long long)need,
@@ -506,8 +611,10 @@ extern "C" int64_t pkv_decode_workspace_bytes(int32_t n_seqs, int32_t n_slots,
                                               int32_t n_heads, int32_t n_kv_heads,
                                               int32_t head_dim) {
   if (n_seqs <= 0 || n_kv_heads <= 0 || n_slots <= 0) return 0;
+  if (n_heads % n_kv_heads) return 0;
   const int64_t counters = ((int64_t)n_seqs * n_kv_heads * 4 + 255) / 256 * 256;
-  return counters + (int64_t)n_slots * n_heads * (head_dim + 2) * 4;
+  const int64_t po = (int64_t)n_slots * n_kv_heads * part_floats(n_heads / n_kv_heads, head_dim);
+  return counters + (po + (int64_t)n_slots * n_heads * 2) * 4;
 }
 
 extern "C" int pkv_attend_decode(const void* q, void* out, void* k_pool, void* v_pool,
@@ -543,6 +650,7 @@ extern "C" int pkv_attend_decode(const void* q, void* out, void* k_pool, void* v
   float* po = nullptr;
   float* pml = nullptr;
   int32_t* cnt = nullptr;
+  uint32_t o_bytes = 0, ml_bytes = 0;
   if (n_slots > 0) {
     const int64_t need =
         pkv_decode_workspace_bytes(n_seqs, n_slots, n_heads, n_kv_heads, head_dim);
@@ -550,16 +658,22 @@ extern "C" int pkv_attend_decode(const void* q, void* out, void* k_pool, void* v
       return fail(PKV_ERR_CAPACITY, "split-K plan needs %lld 256-byte-aligned workspace "
                   "bytes, got %lld", (long long)need, (long long)workspace_bytes);
     // [arrival counters, n_seqs * n_kv_heads, zero before the first launch and
-    //  left zero by every launch][n_slots][Hq][D] partial outputs, then
-    //  [n_slots][Hq][2] (m, l)
+    //  left zero by every launch][n_slots][Hkv][part_floats] partial outputs,
+    //  then [n_slots][Hq][2] (m, l)
+    const int64_t pf = (int64_t)n_slots * n_kv_heads * part_floats(G, head_dim);
+    const int64_t mlf = (int64_t)n_slots * n_heads * 2;
+    if ((pf + mlf) * 4 > 0x7fffffffLL)
+      return fail(PKV_ERR_INVALID, "split-K partials exceed 2 GiB; use larger partitions");
     cnt = (int32_t*)workspace;
     po = (float*)((char*)workspace + ((int64_t)n_seqs * n_kv_heads * 4 + 255) / 256 * 256);
-    pml = po + (int64_t)n_slots * n_heads * head_dim;
+    pml = po + pf;
+    o_bytes = (uint32_t)(pf * 4);
+    ml_bytes = (uint32_t)(mlf * 4);
   }
   if ((int64_t)n_work * n_kv_heads > 0x7fffffffLL)
     return fail(PKV_ERR_INVALID, "too many work items");
   fn(q, out, k_pool, v_pool, num_blocks, kv_indices, plan, n_work, n_kv_heads, scale * kLog2e,
-     k_new, v_new, slot_mapping, po, pml, cnt, status_word, s);
+     k_new, v_new, slot_mapping, po, pml, o_bytes, ml_bytes, cnt, status_word, s);
   PKV_LAUNCH_CHECK();
   return PKV_OK;
 }

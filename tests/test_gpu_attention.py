@@ -109,7 +109,7 @@ def test_prefill_then_decode_across_page_boundaries(geom, dtype):
     check(p.step(grow_and_assemble(seqs, [1, 5, 0, 1, 9], 16), 7), "mixed", tol, rtol)
 
 
-@pytest.mark.parametrize("part_pages", [2, 4, 8])
+@pytest.mark.parametrize("part_pages", [1, 3, 8, 16, 64])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_decode_long_sequences_split_k(part_pages, dtype):
     """Sequences far longer than one partition: the split-K merge path."""
@@ -335,7 +335,7 @@ def _decode_batch(nb, lens, seed):
     return seqs, grow_and_assemble(seqs, lens, 16)
 
 
-@pytest.mark.parametrize("part_pages", [2, 4, 8])
+@pytest.mark.parametrize("part_pages", [1, 3, 8, 16])
 def test_fused_append_equals_separate_launches(part_pages):
     """Deferred append fused into attend == append kernel then attend, bitwise."""
     print(f"fused vs separate part_pages={part_pages}", flush=True)

@@ -55,7 +55,7 @@ def plan_decode(kv_lens, part_pages, ps=16):
     return indptr, npages, buf[:8 * nw.value].reshape(-1, 8), ns.value
 
 
-@pytest.mark.parametrize("part_pages", [2, 4, 8])
+@pytest.mark.parametrize("part_pages", [1, 3, 8, 16, 64])
 def test_decode_plan_covers_every_page_once(part_pages):
     """Every page of every sequence is in exactly one partition."""
     rng = random.Random(part_pages)
@@ -77,6 +77,21 @@ def test_decode_plan_covers_every_page_once(part_pages):
     assert all(all(c == 1 for c in row) for row in covered)
     assert sorted(slots) == list(range(n_slots)), "partial slots must be dense and unique"
     assert list(work[:, 2]) == sorted(work[:, 2], reverse=True), "longest partitions first"
+
+
+def test_decode_plan_rejects_partitions_beyond_one_wave():
+    lib = _native.load()
+    indptr = np.array([0, 1], np.int32)
+    kvl, last = np.array([16], np.int32), np.array([16], np.int32)
+    out = np.empty(16, np.int32)
+    nw, ns = C.c_int32(), C.c_int32()
+    for bad in (0, 65):
+        rc = lib.pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), 1, 16, bad, ptr(out), 16,
+                                 C.byref(nw), C.byref(ns))
+        with pytest.raises(ValueError, match="part_pages"):
+            _native.check(rc, "plan")
+    assert lib.pkv_decode_fast_path(32, 8, 64, 16, _native.DTYPE_F16, 64) == 1
+    assert lib.pkv_decode_fast_path(32, 8, 64, 16, _native.DTYPE_F16, 65) == 0
 
 
 def test_decode_plan_rejects_inconsistent_metadata():
@@ -131,6 +146,8 @@ def test_backend_validates_before_touching_the_library():
         MI355XBackend(1, 8, 16, 2, 4, 8, dtype=torch.float64)
     with pytest.raises(ValueError, match="GPU device"):
         MI355XBackend(1, 8, 16, 2, 4, 8, device="cpu")
+    with pytest.raises(ValueError, match="part_pages"):
+        MI355XBackend(1, 8, 16, 2, 4, 8, part_pages=65)
 
 
 def test_error_codes_map_to_reference_exception_types():
