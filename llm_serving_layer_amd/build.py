@@ -23,8 +23,12 @@ OBJ_DIR = PKG.parent / "_build"
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
-    # Keep hipcc from emitting packed-fp32 VALU ops (unreliable on these boxes).
+    # No packed-fp32 VALU ops: some of their forms have given silently wrong
+    # results on MI355X, so the kernels are built without them.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: the decode kernel's online softmax
+    # rescales them every page, and the AGPR form would copy them back and forth.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=true",
     "-Wno-unused-result",
 ]
 

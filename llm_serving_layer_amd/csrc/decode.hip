@@ -53,7 +53,7 @@ namespace pkv {
 //  slot (-1: the partition is the whole sequence), kv_len, first token,
 //  n_partitions of the sequence, first slot of the sequence}
 constexpr int kWorkInts = 8;
-constexpr int kWaves = 4;         // KV heads (waves) per workgroup, at most
+constexpr int kMaxWaves = 8;      // waves per workgroup (one per KV head), at most
 constexpr int kMaxPartPages = 64; // a partition's page ids fit one wave-wide load
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -114,290 +114,29 @@ template <int D, int G> struct PartLayout {
   static constexpr int FLOATS = NGR * NDB * 64;  // per (slot, KV head)
 };
 
+// Split-K merge for one KV head h of sequence seq, run by the workgroup that
+// published the last partial. Lanes run over partitions for each head row's
+// max M and sum L; then, 64 partitions at a time, the weights 2^(m_s - M)
+// go to this wave's LDS scratch as [partition][GS rows], and the partial
+// outputs are read in the producers' own layout: lane (n, g) takes row group
+// rg = g % NGR of every SPLIT-th partition starting at g / NGR, MB
+// partitions per round trip, and the SPLIT lane groups that share a row
+// group are summed by shuffles at the end. The summation order depends only
+// on the partition count, so the result does not depend on the batch.
 template <typename T, int D, int G>
-__global__ __launch_bounds__(kWaves * 64) void decode_kernel(
-    const T* __restrict__ q, T* __restrict__ out, T* __restrict__ kpool, T* __restrict__ vpool,
-    int64_t num_blocks, const int32_t* __restrict__ kv_indices,
-    const int32_t* __restrict__ work, int32_t n_kv_heads, float scale_log2,
-    const T* __restrict__ k_new, const T* __restrict__ v_new,
-    const int32_t* __restrict__ slot_mapping, float* part_o, float* part_ml,
-    uint32_t o_bytes, uint32_t ml_bytes, int32_t* counters, int32_t* status) {
-  typedef typename Mma<T>::vec8 vec8;
-  typedef typename Mma<T>::vec4 vec4;
+__device__ __forceinline__ void merge_head(T* __restrict__ out, float* wts, int seq, int h,
+                                           int n_kv_heads, int nparts, int slot0,
+                                           __amdgpu_buffer_rsrc_t ro, __amdgpu_buffer_rsrc_t rm) {
   typedef PartLayout<D, G> PL;
-  constexpr int PS = 16;
-  constexpr int GP = D <= 64 ? 4 : 2;   // pages per register tile
-  constexpr int NCH = D / 32;           // QK MFMA k-chunks per page
-  constexpr int NDB = D / 16;           // PV MFMA dim blocks
-  constexpr int VL = D / 8;             // lanes per V row when loading (16 bytes each)
-  constexpr int VROWS = 64 / VL;        // V rows per load instruction
-  constexpr int VLOADS = PS / VROWS;    // load instructions per V page
-  constexpr int TILE = GP * PS * D;     // V tile elements per wave
+  constexpr int NDB = D / 16;
   constexpr int NGR = PL::NGR;
-
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  T* vlds = reinterpret_cast<T*>(smem) + (size_t)wave * TILE;
-
-  const int hw = blockDim.x >> 6;  // KV heads per workgroup
-  const int groups_per_item = n_kv_heads / hw;
-  const int wi = blockIdx.x / groups_per_item;
-  const int h = (blockIdx.x - wi * groups_per_item) * hw + wave;
-  const int32_t* w = work + kWorkInts * wi;
-  const int seq = w[0], pbase = w[1], npp = w[2], slot = w[3];
-  const int kv_len = w[4], tok0 = w[5], nparts = w[6], slot0 = w[7];
-  const int Hq = n_kv_heads * G;
-  const int64_t row = (int64_t)n_kv_heads * D;
-  const int n = lane & 15;   // MFMA row/column within a 16-lane block
-  const int g = lane >> 4;   // MFMA k-group
-  const int vr_ = lane / VL, vc_ = lane % VL;
-
-  // Lane j holds the partition's j-th page id (npp <= 64).
-  int pid = 0;
-  if (lane < npp) pid = kv_indices[pbase + lane];
-  const bool bad = lane < npp && (pid < 0 || (int64_t)pid >= num_blocks);
-  if (bad) pid = 0;
-  if (__builtin_amdgcn_ballot_w64(bad) && lane == 0) flag(status, PKV_STATUS_BAD_PAGE);
-
-  // K/V loads go through a buffer resource per page: the page base is
-  // wave-uniform (scalar registers) and every lane's offset within a page is
-  // the same for all pages, so an address costs one VGPR, not two per load.
-  // The resource's range is the page itself; nt: the pages are streamed once.
-  const uint32_t page_bytes = (uint32_t)(PS * row * (int64_t)sizeof(T));
-  const uint32_t koff = (uint32_t)((n * row + (int64_t)h * D + g * 8) * sizeof(T));
-  const uint32_t voff = (uint32_t)((vr_ * row + (int64_t)h * D + vc_ * 8) * sizeof(T));
-  const uint32_t vstep = (uint32_t)(VROWS * row * sizeof(T));
-  constexpr int kNt = 2;
-  vec8 kt[GP][NCH];
-  vec8 vt[GP][VLOADS];
-  auto load_k = [&](int p0) {
-#pragma unroll
-    for (int j = 0; j < GP; ++j) {
-      if (p0 + j < npp) {
-        const int64_t page = __builtin_amdgcn_readlane(pid, p0 + j);
-        const __amdgpu_buffer_rsrc_t rk = ws_rsrc(kpool + page * PS * row, page_bytes);
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-          kt[j][c] = __builtin_bit_cast(
-              vec8, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + c * 32 * sizeof(T), 0, kNt));
-      }
-    }
-  };
-  auto load_v = [&](int p0) {
-#pragma unroll
-    for (int j = 0; j < GP; ++j) {
-      if (p0 + j < npp) {
-        const int64_t page = __builtin_amdgcn_readlane(pid, p0 + j);
-        const __amdgpu_buffer_rsrc_t rv = ws_rsrc(vpool + page * PS * row, page_bytes);
-#pragma unroll
-        for (int u = 0; u < VLOADS; ++u)
-          vt[j][u] = __builtin_bit_cast(
-              vec8, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, u * vstep, kNt));
-      }
-    }
-  };
-  load_k(0);
-  load_v(0);
-
-  // Q^T as the QK B operand: column n = query head h*G + n (zero beyond G).
-  vec8 qb[NCH];
-  {
-    const T* qr = q + ((int64_t)seq * Hq + h * G + (n < G ? n : 0)) * D + g * 8;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      vec8 t = *reinterpret_cast<const vec8*>(qr + c * 32);
-      qb[c] = (n < G) ? t : vec8{};
-    }
-  }
-
-  // Fused append: the wave whose partition holds the newest token writes its
-  // head's row now; the loaded copy is patched when its page is used.
-  const bool owns_last = k_new != nullptr && tok0 + npp * PS >= kv_len;
-  const int tl = (kv_len - 1) % PS;   // newest token's row within its page
-  bool patch = false;
-  if (owns_last) {
-    const int64_t csr_slot = (int64_t)__builtin_amdgcn_readlane(pid, npp - 1) * PS + tl;
-    const int64_t new_slot = slot_mapping[seq];
-    const bool in_range = new_slot >= 0 && new_slot < num_blocks * PS;
-    if (!in_range && lane == 0) flag(status, PKV_STATUS_BAD_SLOT);
-    patch = new_slot == csr_slot;
-    if (in_range) {
-      const T* kn = k_new + ((int64_t)seq * n_kv_heads + h) * D;
-      const T* vn = v_new + ((int64_t)seq * n_kv_heads + h) * D;
-      if (lane < VL) {
-        *reinterpret_cast<vec8*>(kpool + new_slot * row + (int64_t)h * D + lane * 8) =
-            *reinterpret_cast<const vec8*>(kn + lane * 8);
-        *reinterpret_cast<vec8*>(vpool + new_slot * row + (int64_t)h * D + lane * 8) =
-            *reinterpret_cast<const vec8*>(vn + lane * 8);
-      }
-    }
-  }
-
-  const int ng = (npp + GP - 1) / GP;
-  f32x4 o[NDB];
-#pragma unroll
-  for (int b = 0; b < NDB; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;  // per head n (replicated over g)
-
-  for (int gi = 0; gi < ng; ++gi) {
-    const int p0 = gi * GP;
-    if (patch && gi == ng - 1) {
-      const int jj = npp - 1 - p0;  // the newest page within this tile
-      const T* kn = k_new + ((int64_t)seq * n_kv_heads + h) * D;
-      const T* vn = v_new + ((int64_t)seq * n_kv_heads + h) * D;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        if (n == tl) {
-          const vec8 x = *reinterpret_cast<const vec8*>(kn + c * 32 + g * 8);
-#pragma unroll
-          for (int j = 0; j < GP; ++j)  // static indices keep kt in registers
-            if (j == jj) kt[j][c] = x;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < VLOADS; ++u) {
-        if (u * VROWS + vr_ == tl) {
-          const vec8 x = *reinterpret_cast<const vec8*>(vn + vc_ * 8);
-#pragma unroll
-          for (int j = 0; j < GP; ++j)
-            if (j == jj) vt[j][u] = x;
-        }
-      }
-    }
-
-    // S^T per page; lane (n, g) holds tokens 4g..4g+3 of page j for head n.
-    float s[GP][4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < GP; ++j) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      if (p0 + j < npp) {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) acc = Mma<T>::qk(kt[j][c], qb[c], acc);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool live = p0 + j < npp && tok0 + (p0 + j) * PS + 4 * g + i < kv_len;
-        s[j][i] = live ? acc[i] * scale_log2 : -INFINITY;
-        mx = fmaxf(mx, s[j][i]);
-      }
-    }
-    if (gi + 1 < ng) load_k(p0 + GP);  // K registers are free again
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);  // finite: every tile has a live token
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-
-    vec4 p[GP];
-    float ls = 0.f;
-#pragma unroll
-    for (int j = 0; j < GP; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e = __builtin_amdgcn_exp2f(s[j][i] - m_new);
-        ls += e;
-        p[j][i] = (T)e;
-      }
-    }
-    ls += __shfl_xor(ls, 16, 64);
-    ls += __shfl_xor(ls, 32, 64);
-    l_run = l_run * alpha + ls;
-    m_run = m_new;
-
-    // V pages into this wave's LDS tile, row-major [token][dim]; rows past
-    // kv_len are zeroed. The previous tile's transposing reads are done.
-    wave_lds_sync();
-#pragma unroll
-    for (int j = 0; j < GP; ++j) {
-      if (p0 + j < npp) {
-#pragma unroll
-        for (int u = 0; u < VLOADS; ++u) {
-          const int t = u * VROWS + vr_;
-          vec8 x = vt[j][u];
-          if (tok0 + (p0 + j) * PS + t >= kv_len) x = vec8{};
-          *reinterpret_cast<vec8*>(vlds + (j * PS + t) * D + vc_ * 8) = x;
-        }
-      }
-    }
-    if (gi + 1 < ng) load_v(p0 + GP);  // V registers are free again
-
-    // Rescale O: lane (n, g) holds head rows 4g+i, whose factor lives in lane 4g+i.
-    if (gi > 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a = __shfl(alpha, 4 * g + i, 64);
-#pragma unroll
-        for (int b = 0; b < NDB; ++b) o[b][i] *= a;
-      }
-    }
-    wave_lds_sync();
-
-    // O (rows = heads, cols = dims) += P V; B operand by transposing reads.
-#pragma unroll
-    for (int j = 0; j < GP; ++j) {
-      if (p0 + j < npp) {
-        const T* base = vlds + (j * PS + 4 * g + (n >> 2)) * D + 4 * (n & 3);
-#pragma unroll
-        for (int b = 0; b < NDB; ++b) {
-          const i16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + 16 * b));
-          o[b] = Mma<T>::pv(p[j], __builtin_bit_cast(vec4, raw), o[b]);
-        }
-      }
-    }
-  }
-
-  // lane (dim column n, group g) holds heads 4g..4g+3 of dims 16b + n.
-  if (slot < 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * g + i;
-      const float li = __shfl(l_run, r, 64);  // lane r holds head r's sum
-      if (r < G) {
-#pragma unroll
-        for (int b = 0; b < NDB; ++b)
-          out[((int64_t)seq * Hq + h * G + r) * D + 16 * b + n] = (T)(o[b][i] / li);
-      }
-    }
-    return;
-  }
-
-  // ---- split sequence: publish, count, and the last arrival merges --------
-  const __amdgpu_buffer_rsrc_t ro = ws_rsrc(part_o, o_bytes);
-  const uint32_t head_off = (uint32_t)(((int64_t)slot * n_kv_heads + h) * PL::FLOATS * 4);
-  if (g < NGR) {
-#pragma unroll
-    for (int b = 0; b < NDB; ++b)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[b]), ro,
-                                             head_off + ((g * NDB + b) * 16 + n) * 16, 0, kSc1);
-  }
-  if (lane < G) {
-    const __amdgpu_buffer_rsrc_t rm = ws_rsrc(part_ml, ml_bytes);
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l_run}), rm,
-                                          (uint32_t)(((int64_t)slot * Hq + h * G + lane) * 8),
-                                          0, kSc1);
-  }
-  // Every partial store of this wave has completed at the coherence point
-  // before the arrival is counted.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  int32_t* cnt = counters + (int64_t)seq * n_kv_heads + h;
-  int old = 0;
-  if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  old = __builtin_amdgcn_readfirstlane(old);
-  if (old != nparts - 1) return;
-
-  // Last arrival for (seq, h). Lanes run over partitions for each head
-  // row's max M and sum L; then, 64 partitions at a time, the weights
-  // 2^(m_s - M) go to this wave's (now free) LDS tile as [partition][16
-  // rows], and the partial outputs are read in the producers' own layout:
-  // lane (n, g) takes row group rg = g % NGR of every SPLIT-th partition
-  // starting at g / NGR, MB partitions per round trip, and the SPLIT lane
-  // groups that share a row group are summed by shuffles at the end.
   constexpr int SPLIT = 4 / NGR;
-  constexpr int MB = NDB >= 8 ? 2 : 4;
+  constexpr int GS = 4 * NGR;              // weight rows per partition (>= G)
+  constexpr int MB = 1;                    // partitions per lane per round trip
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
   const int rg = g % NGR, so = g / NGR;
-  float* wts = reinterpret_cast<float*>(vlds);  // [64][16]; the tile holds >= 1024 floats
-  const __amdgpu_buffer_rsrc_t rm = ws_rsrc(part_ml, ml_bytes);
+  const int Hq = n_kv_heads * G;
   auto load_ml = [&](int c0, float* mr, float* lr) {
     const bool ok = c0 + lane < nparts;
     const uint32_t b2 = (uint32_t)(((int64_t)(slot0 + (ok ? c0 + lane : 0)) * Hq + h * G) * 8);
@@ -409,6 +148,27 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(
       lr[r] = ok ? ml[1] : 0.f;
     }
   };
+  // The partial outputs of one batch: MB partitions of this lane's stride.
+  auto load_batch = [&](int c0, int s0, f32x4 (*v)[NDB]) {
+    const int cn = min(64, nparts - c0);
+#pragma unroll
+    for (int u = 0; u < MB; ++u) {
+      const int sl = s0 + u * SPLIT;
+      const uint32_t off =
+          (uint32_t)(((int64_t)(slot0 + c0 + (sl < cn ? sl : 0)) * n_kv_heads + h) *
+                     PL::FLOATS * 4);
+#pragma unroll
+      for (int b = 0; b < NDB; ++b)
+        v[u][b] = sl < cn ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                ro, off + ((rg * NDB + b) * 16 + n) * 16, 0, kSc1))
+                          : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  // The first batch does not depend on the maximum: its loads go out with
+  // the (m, l) loads, so a sequence of up to SPLIT * MB partitions merges in
+  // one round trip.
+  f32x4 v[MB][NDB];
+  load_batch(0, so, v);
   float mr[G], lr[G], M[G], L[G];
 #pragma unroll
   for (int r = 0; r < G; ++r) { M[r] = -INFINITY; L[r] = 0.f; }
@@ -422,38 +182,24 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(
   for (int b = 0; b < NDB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int c0 = 0; c0 < nparts; c0 += 64) {
     if (nparts > 64) load_ml(c0, mr, lr);  // else still in registers
-    f32x4 wv4[4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+    for (int r = 0; r < GS; ++r) {
       float wv = 0.f;
       if (r < G) {
         wv = c0 + lane < nparts ? __builtin_amdgcn_exp2f(mr[r] - M[r]) : 0.f;
         L[r] += wave_sum(wv * lr[r]);
       }
-      wv4[r / 4][r % 4] = wv;
+      wts[lane * GS + r] = wv;
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) *reinterpret_cast<f32x4*>(wts + lane * 16 + 4 * k) = wv4[k];
     wave_lds_sync();
     const int cn = min(64, nparts - c0);
     for (int s0 = so; s0 < cn; s0 += SPLIT * MB) {
-      f32x4 v[MB][NDB];
-#pragma unroll
-      for (int u = 0; u < MB; ++u) {
-        const int sl = s0 + u * SPLIT;
-        const uint32_t off = (uint32_t)(((int64_t)(slot0 + c0 + (sl < cn ? sl : 0)) * n_kv_heads + h) *
-                                        PL::FLOATS * 4);
-#pragma unroll
-        for (int b = 0; b < NDB; ++b)
-          v[u][b] = sl < cn ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                  ro, off + ((rg * NDB + b) * 16 + n) * 16, 0, kSc1))
-                            : f32x4{0.f, 0.f, 0.f, 0.f};
-      }
+      if (c0 > 0 || s0 > so) load_batch(c0, s0, v);
 #pragma unroll
       for (int u = 0; u < MB; ++u) {
         const int sl = s0 + u * SPLIT;
         if (sl < cn) {
-          const f32x4 wr = *reinterpret_cast<const f32x4*>(wts + sl * 16 + 4 * rg);
+          const f32x4 wr = *reinterpret_cast<const f32x4*>(wts + sl * GS + 4 * rg);
 #pragma unroll
           for (int b = 0; b < NDB; ++b) acc[b] += wr * v[u][b];
         }
@@ -484,27 +230,309 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(
       }
     }
   }
-  if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-static int heads_per_workgroup(int Hkv) {
-  for (int c = kWaves; c > 1; --c)
-    if (Hkv % c == 0) return c;
-  return 1;
+// One workgroup per partition, covering every KV head: NW = n_kv_heads / HPW
+// waves, wave w owning heads w, w + NW, ... Each page (16 token rows of all
+// heads, contiguous in the pool) is loaded as whole rows -- lane chunk k is
+// bytes [16 (tid + k NW 64), +16) of the page, so every wave instruction
+// reads whole 128-byte lines of consecutive memory -- into registers two
+// pages ahead, copied into a padded LDS tile, and each wave reads its heads'
+// columns from there: K rows as the A operand of the QK MFMA (ds_read_b128),
+// V through ds_read_b64_tr_b16 as the B operand of the PV MFMA.
+template <typename T, int D, int G, int HPW>
+__global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
+    const T* __restrict__ q, T* __restrict__ out, T* __restrict__ kpool, T* __restrict__ vpool,
+    int64_t num_blocks, const int32_t* __restrict__ kv_indices,
+    const int32_t* __restrict__ work, int32_t n_kv_heads, float scale_log2,
+    const T* __restrict__ k_new, const T* __restrict__ v_new,
+    const int32_t* __restrict__ slot_mapping, float* part_o, float* part_ml,
+    uint32_t o_bytes, uint32_t ml_bytes, int32_t* counters, int32_t* status) {
+  typedef typename Mma<T>::vec8 vec8;
+  typedef typename Mma<T>::vec4 vec4;
+  typedef PartLayout<D, G> PL;
+  constexpr int PS = 16;
+  constexpr int NCH = D / 32;         // QK MFMA k-chunks per head row
+  constexpr int NDB = D / 16;         // PV MFMA dim blocks
+  constexpr int CPL = HPW * D / 32;   // 16-byte chunks per lane per page and tensor
+  constexpr int NGR = PL::NGR;
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int NW = blockDim.x >> 6;
+  const int rowb = n_kv_heads * D * (int)sizeof(T);  // bytes per token row, all heads
+  const int RS = rowb + 16;                          // padded LDS row stride
+  // Two page buffers, each [16][RS] K rows then [16][RS] V rows.
+  constexpr int kBufs = 2;
+  // past both the page tiles and the merge scratch (see decode_lds_bytes)
+  int* s_flag = reinterpret_cast<int*>(smem + max(kBufs * 2 * PS * RS, NW * 64 * 4 * NGR * 4));
+
+  const int32_t* w = work + kWorkInts * blockIdx.x;
+  const int seq = w[0], pbase = w[1], npp = w[2], slot = w[3];
+  const int kv_len = w[4], tok0 = w[5], nparts = w[6], slot0 = w[7];
+  const int Hq = n_kv_heads * G;
+  const int64_t row = (int64_t)n_kv_heads * D;
+  const int n = lane & 15;   // MFMA row/column within a 16-lane block
+  const int g = lane >> 4;   // MFMA k-group
+
+  // Lane j holds the partition's j-th page id (npp <= 64).
+  int pid = 0;
+  if (lane < npp) pid = kv_indices[pbase + lane];
+  const bool bad = lane < npp && (pid < 0 || (int64_t)pid >= num_blocks);
+  if (bad) pid = 0;
+  if (__builtin_amdgcn_ballot_w64(bad) && tid == 0) flag(status, PKV_STATUS_BAD_PAGE);
+
+  // This lane's chunks of a page: byte offset in the page, token row, LDS offset.
+  const int cpr = rowb / 16;
+  uint32_t goff[CPL], loff[CPL];
+  int lrow[CPL];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int c = tid + k * NW * 64;
+    lrow[k] = c / cpr;
+    goff[k] = (uint32_t)c * 16;
+    loff[k] = (uint32_t)(lrow[k] * RS + (c - lrow[k] * cpr) * 16);
+  }
+  const uint32_t page_bytes = (uint32_t)(PS * rowb);
+  constexpr int kNt = 2;
+  auto load_page = [&](int j, vec8* kr, vec8* vr) {
+    const int64_t page = __builtin_amdgcn_readlane(pid, j);
+    const __amdgpu_buffer_rsrc_t rk = ws_rsrc(kpool + page * PS * row, page_bytes);
+    const __amdgpu_buffer_rsrc_t rv = ws_rsrc(vpool + page * PS * row, page_bytes);
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      kr[k] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(rk, goff[k], 0, kNt));
+      vr[k] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(rv, goff[k], 0, kNt));
+    }
+  };
+  vec8 kA[CPL], vA[CPL], kB[CPL], vB[CPL];
+  load_page(0, kA, vA);
+  if (npp > 1) load_page(1, kB, vB);
+
+  // Q^T as the QK B operand per owned head: column n = query head h*G + n.
+  vec8 qb[HPW][NCH];
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    const int h = wave + hh * NW;
+    const T* qr = q + ((int64_t)seq * Hq + h * G + (n < G ? n : 0)) * D + g * 8;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      vec8 t = *reinterpret_cast<const vec8*>(qr + c * 32);
+      qb[hh][c] = (n < G) ? t : vec8{};
+    }
+  }
+
+  // Fused append: the workgroup whose partition holds the newest token writes
+  // that row (all heads) to slot_mapping's slot now; the loaded copy of the
+  // row is patched before it reaches LDS.
+  const bool owns_last = k_new != nullptr && tok0 + npp * PS >= kv_len;
+  const int tl = (kv_len - 1) % PS;   // newest token's row within its page
+  bool patch = false;
+  if (owns_last) {
+    const int64_t csr_slot = (int64_t)__builtin_amdgcn_readlane(pid, npp - 1) * PS + tl;
+    const int64_t new_slot = slot_mapping[seq];
+    const bool in_range = new_slot >= 0 && new_slot < num_blocks * PS;
+    if (!in_range && tid == 0) flag(status, PKV_STATUS_BAD_SLOT);
+    patch = new_slot == csr_slot;
+    if (in_range) {
+      const unsigned char* kn = reinterpret_cast<const unsigned char*>(k_new + seq * row);
+      const unsigned char* vn = reinterpret_cast<const unsigned char*>(v_new + seq * row);
+      unsigned char* kd = reinterpret_cast<unsigned char*>(kpool + new_slot * row);
+      unsigned char* vd = reinterpret_cast<unsigned char*>(vpool + new_slot * row);
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        if (lrow[k] == tl) {
+          const uint32_t col = goff[k] - (uint32_t)tl * rowb;
+          *reinterpret_cast<vec8*>(kd + col) = *reinterpret_cast<const vec8*>(kn + col);
+          *reinterpret_cast<vec8*>(vd + col) = *reinterpret_cast<const vec8*>(vn + col);
+        }
+      }
+    }
+  }
+
+  f32x4 o[HPW][NDB];
+  float m_run[HPW], l_run[HPW];  // per head column n (replicated over g)
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    m_run[hh] = -INFINITY;
+    l_run[hh] = 0.f;
+#pragma unroll
+    for (int b = 0; b < NDB; ++b) o[hh][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Page j lives in LDS buffer j % 2. Step j writes page j+1 (already in
+  // registers) into the other buffer, refills those registers with page j+3,
+  // runs every wave's heads over page j, and ends with the one barrier of the
+  // step: page j+1 is then complete and page j's buffer free for page j+2.
+  auto stage = [&](int j, vec8* kr, vec8* vr) {
+    unsigned char* kl = smem + (j & 1) * 2 * PS * RS;
+    unsigned char* vl = kl + PS * RS;
+    if (patch && j == npp - 1) {
+      const unsigned char* kn = reinterpret_cast<const unsigned char*>(k_new + seq * row);
+      const unsigned char* vn = reinterpret_cast<const unsigned char*>(v_new + seq * row);
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        if (lrow[k] == tl) {
+          const uint32_t col = goff[k] - (uint32_t)tl * rowb;
+          kr[k] = *reinterpret_cast<const vec8*>(kn + col);
+          vr[k] = *reinterpret_cast<const vec8*>(vn + col);
+        }
+      }
+    }
+    const int tp = tok0 + j * PS;  // first token of the page
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      *reinterpret_cast<vec8*>(kl + loff[k]) = kr[k];
+      // rows past kv_len are zeroed so stale bits never reach the PV sum
+      *reinterpret_cast<vec8*>(vl + loff[k]) = tp + lrow[k] < kv_len ? vr[k] : vec8{};
+    }
+  };
+  auto compute = [&](int j) {
+    const unsigned char* kl = smem + (j & 1) * 2 * PS * RS;
+    const unsigned char* vl = kl + PS * RS;
+    const int tp = tok0 + j * PS;
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      const int h = wave + hh * NW;
+      // S^T: lane (n, g) gets the scores of tokens 4g..4g+3 for head n.
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      const unsigned char* kp = kl + n * RS + (h * D + g * 8) * (int)sizeof(T);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        acc = Mma<T>::qk(*reinterpret_cast<const vec8*>(kp + c * 32 * sizeof(T)), qb[hh][c], acc);
+      float sc[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = tp + 4 * g + i < kv_len ? acc[i] * scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sc[i]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run[hh], mx);  // finite: every page has a live token
+      const float alpha = __builtin_amdgcn_exp2f(m_run[hh] - m_new);
+      vec4 p;
+      float ls = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f(sc[i] - m_new);
+        ls += e;
+        p[i] = (T)e;
+      }
+      ls += __shfl_xor(ls, 16, 64);
+      ls += __shfl_xor(ls, 32, 64);
+      l_run[hh] = l_run[hh] * alpha + ls;
+      m_run[hh] = m_new;
+      // lane (n, g) holds output rows 4g+i, whose factor lives in lane 4g+i
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+        for (int b = 0; b < NDB; ++b) o[hh][b][i] *= a;
+      }
+      const unsigned char* vp =
+          vl + (4 * g + (n >> 2)) * RS + (h * D + 4 * (n & 3)) * (int)sizeof(T);
+#pragma unroll
+      for (int b = 0; b < NDB; ++b) {
+        const i16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(vp + 16 * b * sizeof(T)));
+        o[hh][b] = Mma<T>::pv(p, __builtin_bit_cast(vec4, raw), o[hh][b]);
+      }
+    }
+  };
+  // Registers: set A holds the even pages, set B the odd ones.
+  stage(0, kA, vA);
+  if (npp > 2) load_page(2, kA, vA);
+  __syncthreads();
+  for (int j = 0; j < npp; j += 2) {  // two register sets, so unrolled by two
+    if (j + 1 < npp) stage(j + 1, kB, vB);
+    if (j + 3 < npp) load_page(j + 3, kB, vB);
+    compute(j);
+    __syncthreads();
+    if (j + 1 < npp) {
+      if (j + 2 < npp) stage(j + 2, kA, vA);
+      if (j + 4 < npp) load_page(j + 4, kA, vA);
+      compute(j + 1);
+      __syncthreads();
+    }
+  }
+
+  // lane (dim column n, group g) holds heads 4g..4g+3 of dims 16b + n.
+  if (slot < 0) {
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      const int h = wave + hh * NW;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * g + i;
+        const float li = __shfl(l_run[hh], r, 64);  // lane r holds head r's sum
+        if (r < G) {
+#pragma unroll
+          for (int b = 0; b < NDB; ++b)
+            out[((int64_t)seq * Hq + h * G + r) * D + 16 * b + n] = (T)(o[hh][b][i] / li);
+        }
+      }
+    }
+    return;
+  }
+
+  // ---- split sequence: publish, count, and the last arrival merges --------
+  const __amdgpu_buffer_rsrc_t ro = ws_rsrc(part_o, o_bytes);
+  const __amdgpu_buffer_rsrc_t rm = ws_rsrc(part_ml, ml_bytes);
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    const int h = wave + hh * NW;
+    const uint32_t head_off = (uint32_t)(((int64_t)slot * n_kv_heads + h) * PL::FLOATS * 4);
+    if (g < NGR) {
+#pragma unroll
+      for (int b = 0; b < NDB; ++b)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[hh][b]), ro,
+                                               head_off + ((g * NDB + b) * 16 + n) * 16, 0, kSc1);
+    }
+    if (lane < G)
+      __builtin_amdgcn_raw_buffer_store_b64(
+          __builtin_bit_cast(u32x2, f32x2{m_run[hh], l_run[hh]}), rm,
+          (uint32_t)(((int64_t)slot * Hq + h * G + lane) * 8), 0, kSc1);
+  }
+  // Every partial store of every wave has completed at the coherence point
+  // before the workgroup counts its arrival.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  int32_t* cnt = counters + seq;
+  if (tid == 0)
+    *s_flag = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (*s_flag != nparts - 1) return;
+
+  // Last arrival for seq: each wave merges its heads, using its share of
+  // the (now free) page tile as scratch for the weights.
+  float* wts = reinterpret_cast<float*>(smem) + wave * 64 * (4 * NGR);
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh)
+    merge_head<T, D, G>(out, wts, seq, wave + hh * NW, n_kv_heads, nparts, slot0, ro, rm);
+  if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <typename T, int D, int G>
+// Dynamic LDS of a decode workgroup: two padded K+V page buffers plus the
+// arrival flag. The merge reuses the tiles as 64 x 4*ceil(G/4) floats per wave.
+static size_t decode_lds_bytes(int32_t Hkv, int32_t D, int32_t G) {
+  const size_t tiles = 2 * 2 * 16 * (size_t)(Hkv * D * 2 + 16);  // two K+V page buffers
+  const size_t merge = (size_t)std::min(Hkv, kMaxWaves) * 64 * 4 * ((G + 3) / 4) * 4;
+  return std::max(tiles, merge) + 16;  // + the arrival flag
+}
+
+template <typename T, int D, int G, int HPW>
 static void launch(const void* q, void* out, void* kp, void* vp, int64_t nb,
                    const int32_t* indices, const int32_t* work, int32_t n_work, int32_t Hkv,
                    float sl2, const void* kn, const void* vn, const int32_t* slots, float* po,
                    float* pml, uint32_t o_bytes, uint32_t ml_bytes, int32_t* cnt,
                    int32_t* status, hipStream_t s) {
-  constexpr int GP = D <= 64 ? 4 : 2;
-  const int hw = heads_per_workgroup(Hkv);
-  const size_t lds = (size_t)hw * GP * 16 * D * sizeof(T);
-  hipLaunchKernelGGL((decode_kernel<T, D, G>), dim3((unsigned)(n_work * (Hkv / hw))),
-                     dim3(hw * 64), lds, s, (const T*)q, (T*)out, (T*)kp, (T*)vp, nb, indices,
-                     work, Hkv, sl2, (const T*)kn, (const T*)vn, slots, po, pml, o_bytes,
+  const int nw = Hkv / HPW;
+  hipLaunchKernelGGL((decode_kernel<T, D, G, HPW>), dim3((unsigned)n_work), dim3(nw * 64),
+                     decode_lds_bytes(Hkv, D, G), s, (const T*)q, (T*)out, (T*)kp, (T*)vp, nb,
+                     indices, work, Hkv, sl2, (const T*)kn, (const T*)vn, slots, po, pml, o_bytes,
                      ml_bytes, cnt, status);
 }
 
@@ -513,31 +541,39 @@ typedef void (*LaunchFn)(const void*, void*, void*, void*, int64_t, const int32_
                          const int32_t*, float*, float*, uint32_t, uint32_t, int32_t*,
                          int32_t*, hipStream_t);
 
-template <typename T, int D>
+template <typename T, int D, int HPW>
 static LaunchFn pick_g(int G) {
   switch (G) {
-    case 1: return launch<T, D, 1>;
-    case 2: return launch<T, D, 2>;
-    case 4: return launch<T, D, 4>;
-    case 8: return launch<T, D, 8>;
-    case 16: return launch<T, D, 16>;
+    case 1: return launch<T, D, 1, HPW>;
+    case 2: return launch<T, D, 2, HPW>;
+    case 4: return launch<T, D, 4, HPW>;
+    case 8: return launch<T, D, 8, HPW>;
+    case 16: return launch<T, D, 16, HPW>;
     default: return nullptr;
   }
 }
+
+// Heads per wave: the workgroup has one wave per KV head up to kMaxWaves.
+static int heads_per_wave(int Hkv) { return Hkv <= kMaxWaves ? 1 : Hkv / kMaxWaves; }
 
 template <typename T>
-static LaunchFn pick(int D, int G) {
+static LaunchFn pick(int Hkv, int D, int G) {
+  // Whole-row staging needs rows of at most 2 KiB and Hkv a power of two up
+  // to 2 * kMaxWaves (so that waves x heads per wave covers every head).
+  if (Hkv < 1 || Hkv > 2 * kMaxWaves || (Hkv & (Hkv - 1)) || Hkv * D * 2 > 2048) return nullptr;
+  const int hpw = heads_per_wave(Hkv);
   switch (D) {
-    case 64: return pick_g<T, 64>(G);
-    case 128: return pick_g<T, 128>(G);
+    case 64: return hpw == 1 ? pick_g<T, 64, 1>(G) : pick_g<T, 64, 2>(G);
+    case 128: return hpw == 1 ? pick_g<T, 128, 1>(G) : nullptr;
     default: return nullptr;
   }
 }
 
-static LaunchFn fast_decode(int32_t dtype, int32_t D, int32_t G, int32_t page_size, int32_t pp) {
+static LaunchFn fast_decode(int32_t dtype, int32_t Hkv, int32_t D, int32_t G,
+                            int32_t page_size, int32_t pp) {
   if (page_size != 16 || pp < 1 || pp > kMaxPartPages) return nullptr;
-  if (dtype == PKV_DTYPE_F16) return pick<_Float16>(D, G);
-  if (dtype == PKV_DTYPE_BF16) return pick<__bf16>(D, G);
+  if (dtype == PKV_DTYPE_F16) return pick<_Float16>(Hkv, D, G);
+  if (dtype == PKV_DTYPE_BF16) return pick<__bf16>(Hkv, D, G);
   return nullptr;
 }
 
@@ -560,7 +596,8 @@ using namespace pkv;
 extern "C" int pkv_decode_fast_path(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                                     int32_t page_size, int32_t dtype, int32_t part_pages) {
   if (n_kv_heads <= 0 || n_heads % n_kv_heads) return 0;
-  return fast_decode(dtype, head_dim, n_heads / n_kv_heads, page_size, part_pages) ? 1 : 0;
+  return fast_decode(dtype, n_kv_heads, head_dim, n_heads / n_kv_heads, page_size, part_pages)
+             ? 1 : 0;
 }
 
 extern "C" int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_lens,
@@ -632,7 +669,7 @@ extern "C" int pkv_attend_decode(const void* q, void* out, void* k_pool, void* v
   if (n_seqs <= 0) return PKV_OK;
   hipStream_t s = (hipStream_t)stream;
   const int32_t G = n_heads / n_kv_heads;
-  LaunchFn fn = fast_decode(dtype, head_dim, G, page_size, part_pages);
+  LaunchFn fn = fast_decode(dtype, n_kv_heads, head_dim, G, page_size, part_pages);
   if (!fn) {
     if (k_new)
       return fail(PKV_ERR_INVALID, "a fused append needs the fast decode path "
@@ -670,8 +707,6 @@ extern "C" int pkv_attend_decode(const void* q, void* out, void* k_pool, void* v
     o_bytes = (uint32_t)(pf * 4);
     ml_bytes = (uint32_t)(mlf * 4);
   }
-  if ((int64_t)n_work * n_kv_heads > 0x7fffffffLL)
-    return fail(PKV_ERR_INVALID, "too many work items");
   fn(q, out, k_pool, v_pool, num_blocks, kv_indices, plan, n_work, n_kv_heads, scale * kLog2e,
      k_new, v_new, slot_mapping, po, pml, o_bytes, ml_bytes, cnt, status_word, s);
   PKV_LAUNCH_CHECK();
