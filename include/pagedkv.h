@@ -148,6 +148,17 @@ int pkv_plan_prefill(const int32_t* cu_query_lens, const int32_t* kv_indptr,
                      int32_t* plan, int64_t plan_capacity, int32_t* n_tiles_out);
 
 /*
+ * Query tile (tokens per plan tile) for which pkv_attend_prefill runs its
+ * matrix-core kernel on this geometry: 128 / (n_heads / n_kv_heads), so a
+ * tile is 128 query rows of one KV head. 0 if the geometry has no such
+ * kernel (any q_tile then runs the generic kernel). Counterpart of the
+ * tile choice inside FlashInfer's prefill plan
+ * (serving/backends/flashinfer_backend.py:635-649).
+ */
+int pkv_prefill_q_tile(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                       int32_t page_size, int32_t dtype);
+
+/*
  * Paged attention for arbitrary per-sequence query lengths (chunked prefill,
  * mixed prefill+decode) — replaces PagedTorchBackend.attend
  * (serving/backends/paged_torch.py:280-485) and FlashInfer's prefill wrapper
@@ -156,7 +167,9 @@ int pkv_plan_prefill(const int32_t* cu_query_lens, const int32_t* kv_indptr,
  * kv_len_i keys) attends keys [0, kv_len_i - q_len_i + j] (bottom-right
  * causal). q, out: [n_tokens, n_heads, head_dim]. `batch_indices` maps each
  * token to its sequence. `plan` is the device copy of pkv_plan_prefill's
- * output (q_tile must match the one given to the plan).
+ * output (q_tile must match the one given to the plan). The matrix-core
+ * kernel runs when q_tile == pkv_prefill_q_tile(...) != 0; otherwise the
+ * generic kernel runs (it reads cu_query_lens / batch_indices, not the plan).
  */
 int pkv_attend_prefill(const void* q, void* out,
                        const void* k_pool, const void* v_pool, int64_t num_blocks,

@@ -54,7 +54,7 @@ _DTYPES = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16,
 
 DEFAULT_PART_PAGES = 8   # split-K partition: 8 pages = 128 tokens per wave
 MAX_PART_PAGES = 64      # a partition's page ids are read by one wavefront
-DEFAULT_Q_TILE = 64
+DEFAULT_Q_TILE = 64      # prefill tile when the geometry has no matrix-core kernel
 
 
 def is_available() -> bool:
@@ -89,7 +89,7 @@ class MI355XBackend:
     def __init__(self, num_layers: int, num_blocks: int, block_size: int, n_kv_heads: int,
                  n_heads: int, head_dim: int, device: str | torch.device = "cuda:0",
                  dtype: torch.dtype = torch.float16, *,
-                 part_pages: int = DEFAULT_PART_PAGES, q_tile: int = DEFAULT_Q_TILE,
+                 part_pages: int = DEFAULT_PART_PAGES, q_tile: int | None = None,
                  fuse_append: bool = True):
         if n_heads % n_kv_heads != 0:
             raise ValueError(
@@ -106,6 +106,8 @@ class MI355XBackend:
                              f"got {dtype}")
         if head_dim > 256:
             raise ValueError(f"head_dim={head_dim} > 256 is not supported")
+        if q_tile is not None and q_tile < 1:
+            raise ValueError(f"q_tile={q_tile} must be positive")
         if not 1 <= part_pages <= MAX_PART_PAGES:
             raise ValueError(f"part_pages={part_pages} must be in [1, {MAX_PART_PAGES}]")
         try:
@@ -129,7 +131,11 @@ class MI355XBackend:
         self.dtype = dtype
         self.groups = n_heads // n_kv_heads
         self.part_pages = part_pages
-        self.q_tile = q_tile
+        # The matrix-core prefill kernel owns 128 query rows (tokens x heads)
+        # of one KV head; other geometries run the generic kernel.
+        self._prefill_tile = int(self._lib.pkv_prefill_q_tile(
+            n_heads, n_kv_heads, head_dim, block_size, _DTYPES[dtype]))
+        self.q_tile = q_tile or self._prefill_tile or DEFAULT_Q_TILE
         self._code = _DTYPES[dtype]
         self._fast_decode = bool(self._lib.pkv_decode_fast_path(
             n_heads, n_kv_heads, head_dim, block_size, self._code, part_pages))

@@ -2,7 +2,9 @@
 // mixed prefill + decode), and the generic fallback used for any geometry
 // the fast kernels do not cover.
 //
-//  * generic_kernel — any geometry, any query length, bottom-right causal.
+//  * generic_kernel — any geometry, any query length, bottom-right causal;
+//    used when prefill.hip's MFMA kernel does not cover the geometry or the
+//    plan was tiled for another query tile.
 //
 // Numerics follow serving/backends/paged_torch.py:443-485: scores and
 // softmax in fp32, probabilities rounded to the pool dtype, PV accumulated
@@ -13,6 +15,13 @@
 #include "pkv_common.h"
 
 namespace pkv {
+
+int run_fast_prefill(const void* q, void* out, const void* kp, const void* vp, int64_t nb,
+                     const int32_t* cu_q, const int32_t* indptr, const int32_t* indices,
+                     const int32_t* kv_lens, int32_t Hq, int32_t Hkv, int32_t D,
+                     int32_t page_size, float scale, int32_t dtype, const int32_t* plan,
+                     int32_t n_tiles, int32_t q_tile, int32_t* status, hipStream_t s,
+                     bool* ran);
 
 // ------------------------------------------------------------------ plans ---
 
@@ -216,9 +225,13 @@ extern "C" int pkv_attend_prefill(const void* q, void* out, const void* k_pool,
                                   int32_t q_tile, int32_t* status_word, void* stream) {
   int rc = check_geometry(n_heads, n_kv_heads, head_dim, page_size, dtype);
   if (rc) return rc;
-  (void)plan; (void)n_tiles; (void)q_tile;
   if (n_tokens <= 0) return PKV_OK;
   hipStream_t s = (hipStream_t)stream;
+  bool ran = false;
+  rc = run_fast_prefill(q, out, k_pool, v_pool, num_blocks, cu_query_lens, kv_indptr, kv_indices,
+                        kv_lens, n_heads, n_kv_heads, head_dim, page_size, scale, dtype, plan,
+                        n_tiles, q_tile, status_word, s, &ran);
+  if (rc || ran) return rc;
   if (dtype == PKV_DTYPE_F16)
     return launch_generic<_Float16>(q, out, k_pool, v_pool, num_blocks, cu_query_lens, kv_indptr, kv_indices, kv_lens, batch_indices, n_seqs, n_tokens, n_heads, n_kv_heads, head_dim, page_size, scale, status_word, s);
   if (dtype == PKV_DTYPE_BF16)

@@ -3,40 +3,42 @@
 // Work decomposition (planned on the host once per batch): a sequence's
 // pages are cut into partitions of at most part_pages pages (split-K over
 // the KV axis; the split depends only on that sequence's own length, so its
-// result never depends on what it is batched with). A workgroup owns one
-// partition and its waves own one KV head each, so they request the same
-// pages together (the heads of a token row are adjacent in memory).
+// result never depends on what it is batched with). One workgroup owns one
+// partition for every KV head: one wave per KV head (two heads per wave
+// beyond 8 KV heads).
 //
-// A wave walks its partition GP pages at a time with an online softmax, and
-// the next GP pages are always in flight while the current ones are used:
-// the K registers are refilled as soon as S is computed, the V registers as
-// soon as V has been copied to LDS. Per GP pages (G query heads share the KV
-// head, G <= 16):
-//  1. S^T = K Q^T with one 16x16x32 MFMA per 32 dims of a 16-token page: the
-//     K rows ARE the A operand (lane (token m, group g) holds 16 contiguous
-//     bytes of row m), Q^T the B operand (column n = query head n, zero
+// Memory: a page is 16 token rows x (all KV heads x head_dim) contiguous in
+// the pool. The workgroup reads it as whole rows -- lane chunk k is bytes
+// [16 (tid + k * threads), +16) of the page -- so each wave instruction
+// covers consecutive 128-byte lines, the pattern that streams fastest. The
+// pages arrive in registers two pages ahead of use, are copied to one of two
+// padded LDS page buffers, and one barrier per page separates filling a
+// buffer from reading it.
+//
+// Per wave, head and page (G query heads share the KV head, G <= 16):
+//  1. S^T = K Q^T with one 16x16x32 MFMA per 32 dims: the K rows (from LDS)
+//     are the A operand, Q^T the B operand (column n = query head n, zero
 //     beyond G). Lane (head n, group g) then holds the scores of tokens
 //     4g..4g+3 of the page for head n;
-//  2. softmax in registers: mask past kv_len, running max / sum with one
-//     in-lane pass plus two cross-lane steps; p = 2^(s*scale*log2e - m)
-//     rounded to the pool dtype -- four values per lane that are exactly the
-//     A operand of a 16x16x16 MFMA;
-//  3. PV on MFMA: the V pages go to LDS row-major and ds_read_b64_tr_b16
-//     hands each lane 4 consecutive tokens of one dim, the B operand, one
-//     read per 16 dims. Tokens past kv_len are zeroed so stale bits can
-//     never reach the sum.
+//  2. online softmax in registers: mask past kv_len, running max / sum with
+//     two cross-lane steps; p = 2^(s*scale*log2e - m) rounded to the pool
+//     dtype -- four values per lane that are exactly the A operand of a
+//     16x16x16 MFMA;
+//  3. PV on MFMA: ds_read_b64_tr_b16 hands each lane 4 consecutive tokens of
+//     one V dim, the B operand, one read per 16 dims. V rows past kv_len are
+//     zeroed in LDS so stale bits can never reach the sum.
 //
 // Split sequences merge in the same launch. Each partition publishes its
 // partial (o, m, l) with 16-byte buffer stores carrying the sc1 (agent
 // coherence) bit, which write through the per-XCD L2, waits until they have
-// completed (s_waitcnt vmcnt(0)), then bumps an arrival counter for its
-// (sequence, KV head). The wave that sees the last arrival reads the
-// partials back with sc1 loads (never a stale L2 line) and writes the
-// output. This avoids a second launch and an agent-scope release fence,
-// whose L2 write-back walks the whole cache.
+// completed (s_waitcnt vmcnt(0)), then bumps its sequence's arrival counter.
+// The workgroup that sees the last arrival reads the partials back with sc1
+// loads (never a stale L2 line) and writes the output. This avoids a second
+// launch and an agent-scope release fence, whose L2 write-back walks the
+// whole cache.
 //
 // Fused append (optional): when the caller passes the step's new K/V rows,
-// the wave that owns a sequence's last page writes the row of its head to
+// the workgroup that owns a sequence's last page writes the new row to
 // slot_mapping's slot and patches the copy it loaded, so a decode step costs
 // one launch per layer instead of two. The patch is applied only when
 // slot_mapping names the same slot as the page table, so the result is
@@ -45,7 +47,7 @@
 #include <algorithm>
 #include <vector>
 
-#include "pkv_common.h"
+#include "mfma.h"
 
 namespace pkv {
 
@@ -55,54 +57,6 @@ namespace pkv {
 constexpr int kWorkInts = 8;
 constexpr int kMaxWaves = 8;      // waves per workgroup (one per KV head), at most
 constexpr int kMaxPartPages = 64; // a partition's page ids fit one wave-wide load
-
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-
-template <typename T> struct Mma;
-template <> struct Mma<_Float16> {
-  typedef f16x8 vec8;
-  typedef f16x4 vec4;
-  __device__ static f32x4 qk(vec8 a, vec8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-  __device__ static f32x4 pv(vec4 a, vec4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-  }
-};
-template <> struct Mma<__bf16> {
-  typedef bf16x8 vec8;
-  typedef bf16x4 vec4;
-  __device__ static f32x4 qk(vec8 a, vec8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  __device__ static f32x4 pv(vec4 a, vec4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
-                                                    __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
-  }
-};
-
-// Orders this wave's LDS writes before its own (cross-lane) LDS reads. A
-// wave's LDS operations execute in order, so a compiler-level barrier with
-// wavefront-scope fences is all that is needed (no s_barrier).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Buffer resource over the split-K workspace: raw (untyped) 32-bit records,
-// hardware range check against `bytes` (out-of-range loads read 0, stores
-// are dropped). kSc1 on a load/store = agent-scope coherent access.
-constexpr int kSc1 = 16;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
-}
 
 // Layout of one partition's partial output: per (slot, KV head), NGR groups
 // of 4 head rows, each NDB dim blocks of 16 lanes x 4 rows (float4 per
@@ -296,7 +250,6 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     loff[k] = (uint32_t)(lrow[k] * RS + (c - lrow[k] * cpr) * 16);
   }
   const uint32_t page_bytes = (uint32_t)(PS * rowb);
-  constexpr int kNt = 2;
   auto load_page = [&](int j, vec8* kr, vec8* vr) {
     const int64_t page = __builtin_amdgcn_readlane(pid, j);
     const __amdgpu_buffer_rsrc_t rk = ws_rsrc(kpool + page * PS * row, page_bytes);

@@ -34,9 +34,9 @@ class Pair:
     """The GPU backend and the CPU fp32 oracle fed identical (dtype-rounded) inputs."""
 
     def __init__(self, num_layers, num_blocks, block_size, n_kv, n_heads, head_dim,
-                 dtype=torch.float16, part_pages=4):
+                 dtype=torch.float16, part_pages=4, q_tile=None):
         self.gpu = MI355XBackend(num_layers, num_blocks, block_size, n_kv, n_heads, head_dim,
-                                 device=DEV, dtype=dtype, part_pages=part_pages)
+                                 device=DEV, dtype=dtype, part_pages=part_pages, q_tile=q_tile)
         self.ref = PagedTorchOracle(num_layers, num_blocks, block_size, n_kv, n_heads, head_dim,
                                     device="cpu", dtype=torch.float32)
         self.dtype = dtype
@@ -123,6 +123,64 @@ def test_decode_long_sequences_split_k(part_pages, dtype):
     meta = grow_and_assemble(seqs, [1] * 6, 16)
     tol, rtol = (2e-3, 1e-2) if dtype == torch.float16 else (1.6e-2, 8e-2)
     check(p.step(meta, 3), "split-K", tol, rtol)
+
+
+def _shared_prefix_batch(alloc, n_seqs, prefix_tokens):
+    """Radix-style sharing: n_seqs tables start with the same prefix blocks
+    (refcounted); each then grows its own blocks."""
+    pre = SequenceBlocks(alloc, seq_id=100)
+    pre.append(prefix_tokens)
+    seqs = []
+    for i in range(n_seqs):
+        s = SequenceBlocks(alloc, seq_id=i)
+        alloc.incref(pre.block_ids)
+        s.block_ids = list(pre.block_ids)
+        s.num_tokens = prefix_tokens
+        seqs.append(s)
+    return pre, seqs
+
+
+@pytest.mark.parametrize("geom", [(8, 32, 64), (2, 8, 128), (8, 8, 64), (1, 16, 64),
+                                  (4, 8, 64)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_chunked_prefill_over_shared_prefix(geom, dtype):
+    """The chunked-prefill workload at reduced size: a prefix written once,
+    shared by every table, then each sequence appends its own query chunk
+    (causal within the chunk, full attention to the prefix)."""
+    n_kv, n_heads, d = geom
+    print(f"shared-prefix prefill geom={geom} dtype={dtype}", flush=True)
+    p = Pair(2, 256, 16, n_kv, n_heads, d, dtype=dtype)
+    assert p.gpu.q_tile == 128 // (n_heads // n_kv), "matrix-core prefill expected"
+    alloc, _keep = fragmented_allocator(256, 16)
+    # a whole number of pages, as a radix cache shares them (a partial last
+    # page would be copied on write before a sequence appends into it)
+    pre, seqs = _shared_prefix_batch(alloc, 3, 192)
+    tol, rtol = (2e-3, 1e-2) if dtype == torch.float16 else (1.6e-2, 8e-2)
+    check(p.step(make_meta([pre], [192], 16), 5, kv_scale=0.5), "prefix", tol, rtol)
+    meta = grow_and_assemble(seqs, [150, 77, 1], 16)
+    check(p.step(meta, 6, kv_scale=0.5), "chunk over shared prefix", tol, rtol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_matrix_core_prefill_matches_generic_kernel(dtype):
+    """Same batch through the MFMA prefill (default tile) and the generic
+    kernel (a tile the MFMA kernel does not take): both within the bar of
+    the oracle, and of each other."""
+    print(f"mfma vs generic prefill dtype={dtype}", flush=True)
+    outs = []
+    for q_tile in (None, 17):
+        p = Pair(1, 256, 16, 8, 32, 64, dtype=dtype, q_tile=q_tile)
+        p.poison(3)
+        alloc, _keep = fragmented_allocator(256, 16)
+        seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(4)]
+        for s, n in zip(seqs, [5, 40, 0, 130]):
+            s.append(n)
+        res = p.step(grow_and_assemble(seqs, [300, 33, 64, 1], 16), 9)
+        tol, rtol = (2e-3, 1e-2) if dtype == torch.float16 else (1.6e-2, 8e-2)
+        check(res, f"q_tile={q_tile}", tol, rtol)
+        outs.append(res[0][1].float())
+    diff = (outs[0] - outs[1]).abs().max().item()
+    assert diff <= (4e-3 if dtype == torch.float16 else 3.2e-2), diff
 
 
 def test_config1_fp16_fast_path_and_fp32_fixture():
