@@ -1,29 +1,45 @@
 #!/usr/bin/env python3
 """
-Decode-step benchmark of the MI355X paged-KV backend.
+Benchmarks of the MI355X paged-KV backend. Prints ONE JSON line.
 
-Workload (one "step"): Llama-3.2-1B attention geometry (32 query heads,
-8 KV heads, head_dim 64), block_size 16, fp16, batch 256 with per-sequence
-context lengths drawn lognormal (mean 256, sigma 0.8, clipped to [1, 2048],
-seed 20260731 -> realized mean 257.7, p90 498, max 1371, 65 980 tokens,
-4247 pages), block tables shuffled over a pool of 2x the pages needed,
-K/V cache and Q ~ N(0,1)*0.5. A step is, for each of the 16 layers, one KV
-append of the new token of every sequence followed by one paged decode
-attention over every sequence's whole history, through the backend's public
-``append_kv`` / ``attend``. All 16 layers are cycled so a layer's KV
-(~135 MB) cannot stay resident in the 256 MB last-level cache.
+Default workload (``--workload decode``), the headline: Llama-3.2-1B
+attention geometry (32 query heads, 8 KV heads, head_dim 64), block_size 16,
+fp16, batch 256 with per-sequence context lengths drawn lognormal (mean 256,
+sigma 0.8, clipped to [1, 2048], seed 20260731 -> realized mean 257.7, p90
+498, max 1371, 65 980 tokens, 4247 pages), block tables shuffled over a pool
+of 2x the pages needed, K/V cache and Q ~ N(0,1)*0.5. A step is, for each of
+the 16 layers, one KV append of every sequence's new token followed by one
+paged decode attention over every sequence's whole history, through the
+backend's public ``append_kv`` / ``attend`` (which run as one fused launch
+per layer). All 16 layers are cycled so a layer's KV (~135 MB) cannot stay
+resident in the 256 MB last-level cache.
 
-Prints ONE JSON line. ``value`` is the algorithmic HBM bytes of the step
-(KV read once per KV head, Q read, O written, append read+write, metadata)
-divided by the measured step time. ``roofline`` is the decode kernel alone,
-timed with HIP events on the stream it is launched on.
+``value`` = algorithmic HBM bytes of the step (KV read once per KV head, Q
+read, O written, append read + write, metadata) / measured step time. The
+step is captured once in a HIP graph and replayed, as a serving engine runs
+its decode steps; the same step issued call by call is reported under
+``eager``. ``roofline`` is the per-layer decode launch.
+
+Other workloads (one JSON line each, same fields):
+  prefill   8 sequences share a 1536-token paged prefix and each appends a
+            512-token chunk (causal in the chunk), 16 layers; TFLOP/s of the
+            masked attention on matrix cores.
+  copy      4096 copy-on-write block pairs per step (27% of sources from a
+            shared-prefix set), every layer, K and V; GB/s.
+  swap      64 sequences x 256 tokens out to pinned host memory and back into
+            different blocks; GB/s per direction over the host link.
+  capacity  decode at 4096 sequences of 16..64 tokens, then 512 sequences of
+            lognormal mean 2048 (clipped to 2048), pool of ~200 GB; GB/s.
+  calib     a 1 GiB device copy, the known-size reference for HBM counters.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
+import random
 import sys
 import time
 from pathlib import Path
@@ -31,47 +47,136 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-HQ, HKV, D, BS, LAYERS, BATCH = 32, 8, 64, 16, 16, 256
+HQ, HKV, D, BS, LAYERS = 32, 8, 64, 16, 16
 SEED = 20260731
 PEAK_HBM_GBPS = 8000.0
+PEAK_MFMA_F16_TFLOPS = 2500.0
 METRIC = ("paged decode attn+append HBM GB/s (% peak); decode tok/s @ batch 256, 1 GPU")
+GEOM = "Llama-3.2-1B attention geometry 32q/8kv/d64, block 16, fp16"
 
 
-def lengths():
-    import math
-    import random
-
-    rng = random.Random(SEED)
-    mu = math.log(256) - 0.8 ** 2 / 2.0
-    return [max(1, min(2048, int(round(rng.lognormvariate(mu, 0.8))))) for _ in range(BATCH)]
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(kv_lens, pages, T):
-    """Per layer: (decode kernel bytes, append kernel bytes)."""
+def lognormal_lengths(n, mean_len, sigma=0.8, max_seq=2048, seed=SEED):
+    """The reference's length law (bench/capacity.py:196-242), lognormal branch."""
+    rng = random.Random(seed)
+    mu = math.log(mean_len) - sigma ** 2 / 2.0
+    return [max(1, min(max_seq, int(round(rng.lognormvariate(mu, sigma))))) for _ in range(n)]
+
+
+def decode_bytes(kv_lens, pages):
+    """Algorithmic HBM bytes of one layer's append + decode attention."""
+    T = len(kv_lens)
     kv = sum(kv_lens) * HKV * D * 2 * 2          # K and V rows, each KV head once
     qo = T * HQ * D * 2 * 2                      # Q read + O written
-    meta = 4 * (pages + 2 * len(kv_lens) + 1)    # kv_indices, kv_lens, kv_indptr
-    append = T * HKV * D * 2 * 2 * 2             # K,V rows read + written
-    return kv + qo + meta, append + 4 * T
+    meta = 4 * (pages + 2 * T + 1)               # kv_indices, kv_lens, kv_indptr
+    append = T * HKV * D * 2 * 2 * 2 + 4 * T     # new K,V rows read + written, slots
+    return kv + qo + meta + append
 
 
-def build(device, lens, part_pages):
+# ----------------------------------------------------------------- helpers ---
+
+def fill_pool(bk, seed):
     import torch
+    g = torch.Generator(device=bk.device).manual_seed(seed)
+    for l in range(bk.num_layers):  # every page read holds real data
+        for kv in range(2):
+            x = bk._pool[l, kv]
+            x.copy_(torch.randn(x.shape, generator=g, device=bk.device, dtype=torch.float32)
+                    .mul_(0.5))
 
-    from llm_serving_layer_amd import BlockAllocator, ScheduledSeq, SequenceBlocks, build_batch_meta
-    from llm_serving_layer_amd.backend import MI355XBackend
 
-    pages = sum(-(-n // BS) for n in lens)
-    nb = 2 * pages
-    bk = MI355XBackend(LAYERS, nb, BS, HKV, HQ, D, device=device, dtype=torch.float16,
-                       part_pages=part_pages)
-    g = torch.Generator(device=device).manual_seed(SEED)
-    for l in range(LAYERS):  # the whole pool, so every page read holds real data
-        bk._pool[l].copy_(torch.randn(bk._pool[l].shape, generator=g, device=device) * 0.5)
+def shuffled_allocator(nb, seed=SEED):
+    import torch
+    from llm_serving_layer_amd import BlockAllocator
     alloc = BlockAllocator(nb, BS)
     alloc.allocate(nb)
-    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(SEED)).tolist()
-    alloc.free(perm)
+    alloc.free(torch.randperm(nb, generator=torch.Generator().manual_seed(seed)).tolist())
+    return alloc
+
+
+def time_eager(step, steps, warmup, per_launch):
+    """K steps through the public API between synchronizations; per-launch
+    HIP events on the current stream (the backend launches there)."""
+    import torch
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(per_launch)] for _ in range(steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for s in range(steps):
+        step(ev[s])
+    stop.record()
+    enqueue = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(stop)
+    launch = [a.elapsed_time(b) for row in ev for a, b in row]
+    return {"ms_per_step": max(gpu_ms, wall * 1e3) / steps,
+            "gpu_ms_per_step": gpu_ms / steps, "wall_ms_per_step": wall * 1e3 / steps,
+            "host_enqueue_ms_per_step": enqueue * 1e3 / steps,
+            "launch_ms": sum(launch) / len(launch)}
+
+
+def time_graph(step, steps, warmup):
+    """The same step captured once in a HIP graph and replayed K times,
+    bracketed by events on the replay stream."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(None)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step(None)
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    gs, ge = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    gs.record()
+    for _ in range(steps):
+        g.replay()
+    ge.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return {"ms_per_step": max(gs.elapsed_time(ge), wall * 1e3) / steps,
+            "gpu_ms_per_step": gs.elapsed_time(ge) / steps}, g
+
+
+def traffic_for(name):
+    f = ROOT / "profiles" / f"{name}_traffic.json"
+    if f.exists():
+        return json.loads(f.read_text()).get("hbm_bytes_per_launch")
+    return None
+
+
+def base_line(args, metric, value, unit, ms, dtype, workload, **cfg):
+    return {"metric": metric, "value": value, "unit": unit, "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": dtype, "data": "synthetic", "config": {"workload": workload, **cfg}}
+
+
+# ------------------------------------------------------------------ decode ---
+
+def decode_setup(device, lens, nb, part_pages):
+    import torch
+    from llm_serving_layer_amd import ScheduledSeq, SequenceBlocks, build_batch_meta
+    from llm_serving_layer_amd.backend import MI355XBackend
+
+    bk = MI355XBackend(LAYERS, nb, BS, HKV, HQ, D, device=device, dtype=torch.float16,
+                       part_pages=part_pages)
+    fill_pool(bk, SEED)
+    alloc = shuffled_allocator(nb)
     seqs = []
     for i, n in enumerate(lens):
         s = SequenceBlocks(alloc, seq_id=i)
@@ -83,10 +188,101 @@ def build(device, lens, part_pages):
     meta = build_batch_meta([ScheduledSeq(s, [0]) for s in seqs], device, BS)
     torch.cuda.synchronize()
     meta_ms = (time.perf_counter() - t0) * 1e3
-    k = (torch.randn(LAYERS, BATCH, HKV, D, generator=g, device=device) * 0.5).half()
-    v = (torch.randn(LAYERS, BATCH, HKV, D, generator=g, device=device) * 0.5).half()
-    q = (torch.randn(LAYERS, BATCH, HQ, D, generator=g, device=device) * 0.5).half()
-    return bk, meta, k, v, q, pages, meta_ms
+    T = len(lens)
+    g = torch.Generator(device=device).manual_seed(SEED + 1)
+    k = (torch.randn(LAYERS, T, HKV, D, generator=g, device=device) * 0.5).half()
+    v = (torch.randn(LAYERS, T, HKV, D, generator=g, device=device) * 0.5).half()
+    q = (torch.randn(LAYERS, T, HQ, D, generator=g, device=device) * 0.5).half()
+
+    def step(events):
+        for l in range(LAYERS):
+            bk.append_kv(l, k[l], v[l], meta)
+            if events is not None:
+                events[l][0].record()
+            bk.attend(q[l], l, 0.125, meta)
+            if events is not None:
+                events[l][1].record()
+
+    return bk, meta, step, meta_ms
+
+
+def run_decode_like(args, lens, nb, label):
+    import torch
+    pages = sum(-(-n // BS) for n in lens)
+    log(f"{label}: {len(lens)} sequences, {sum(lens)} tokens, {pages} pages, pool {nb} blocks")
+    bk, meta, step, meta_ms = decode_setup("cuda:0", lens, nb, args.part_pages)
+    layer_bytes = decode_bytes(lens, pages)
+    step_bytes = LAYERS * layer_bytes
+    log("eager timing")
+    eager = time_eager(step, args.steps, args.warmup, LAYERS)
+    bk.check_device_errors()
+    graph = None
+    if not args.eager:
+        log("graph capture + replay")
+        graph, _g = time_graph(step, args.steps, args.warmup)
+        bk.check_device_errors()
+    # plan + metadata end to end: dropping the plan forces a re-plan
+    t0 = time.perf_counter()
+    bk.invalidate_plan()
+    bk.attend(torch.zeros(len(lens), HQ, D, dtype=torch.float16, device="cuda:0"), 0, 0.125,
+              meta)
+    torch.cuda.synchronize()
+    plan_ms = (time.perf_counter() - t0) * 1e3
+    run = graph or eager
+    ms = run["ms_per_step"]
+    launch_ms = ms / LAYERS if graph else eager["launch_ms"]
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    kern_gbps = layer_bytes / (launch_ms * 1e-3) / 1e9
+    return {
+        "gbps": gbps, "ms": ms, "tok_s": len(lens) / (ms * 1e-3), "pages": pages,
+        "step_bytes": step_bytes, "layer_bytes": layer_bytes, "launch_ms": launch_ms,
+        "kern_gbps": kern_gbps, "eager": eager, "graph": graph, "meta_ms": meta_ms,
+        "plan_ms": plan_ms,
+    }
+
+
+def bench_decode(args):
+    lens = lognormal_lengths(256, 256)
+    r = run_decode_like(args, lens, 2 * sum(-(-n // BS) for n in lens), "decode")
+    e = r["eager"]
+    line = base_line(
+        args, METRIC, round(r["gbps"], 1), "GB/s", r["ms"], "fp16",
+        ("paged decode step: 16 layers x (KV append + paged decode attention), batch 256, "
+         f"{GEOM}, lognormal context lengths mean 258 (seed {SEED})"),
+        batch=256, layers=LAYERS, context_tokens=sum(lens), pages=r["pages"],
+        pool_blocks=2 * r["pages"], part_pages=args.part_pages,
+        execution="hip graph replay" if r["graph"] else "eager")
+    line.update({
+        "pct_peak_hbm": round(100 * r["gbps"] / PEAK_HBM_GBPS, 2),
+        "decode_tok_s": round(r["tok_s"], 1),
+        "algorithmic_bytes_per_step": r["step_bytes"],
+        "eager": {"ms_per_step": round(e["ms_per_step"], 4),
+                  "GB/s": round(r["step_bytes"] / (e["ms_per_step"] * 1e-3) / 1e9, 1),
+                  "decode_tok_s": round(256 / (e["ms_per_step"] * 1e-3), 1),
+                  "gpu_ms_per_step": round(e["gpu_ms_per_step"], 4),
+                  "host_enqueue_ms_per_step": round(e["host_enqueue_ms_per_step"], 4),
+                  "attend_event_avg_ms": round(e["launch_ms"], 5)},
+        "host_side_ms": {"batch_meta_build_upload": round(r["meta_ms"], 3),
+                         "plan_incl_device_to_host_sync": round(r["plan_ms"], 3)},
+        "roofline": {
+            "kernel": "pkv::decode_kernel<_Float16,64,4,1> (KV append fused), one launch per layer",
+            "bound": "hbm", "achieved": round(r["kern_gbps"], 1), "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s", "frac": round(r["kern_gbps"] / PEAK_HBM_GBPS, 4),
+            "traffic": traffic_for("decode_kernel_config2"),
+            "algorithmic_bytes_per_launch": r["layer_bytes"],
+            "avg_launch_ms": round(r["launch_ms"], 5),
+            "timing": ("graph replay time / 16 launches, HIP events on the replay stream"
+                       if r["graph"] else "HIP events around each launch"),
+        },
+    })
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline (oracle)")
+        cpu = cpu_baseline(lens, args.cpu_budget)
+    line["cpu_baseline"] = cpu
+    if cpu:
+        line["gpu_over_cpu"] = round(line["decode_tok_s"] / cpu["value"], 1)
+    return line
 
 
 def cpu_baseline(lens, budget_s=12.0):
@@ -103,6 +299,7 @@ def cpu_baseline(lens, budget_s=12.0):
 
     cores = min(len(os.sched_getaffinity(0)), 16)
     torch.set_num_threads(cores)
+    T = len(lens)
     pages = sum(-(-n // BS) for n in lens)
     ref = PagedTorchOracle(1, pages, BS, HKV, HQ, D, device="cpu", dtype=torch.float32)
     g = torch.Generator().manual_seed(SEED)
@@ -115,8 +312,8 @@ def cpu_baseline(lens, budget_s=12.0):
         s.append(n)
         seqs.append(s)
     meta = build_batch_meta([ScheduledSeq(s, [0]) for s in seqs], "cpu", BS)
-    k = torch.randn(BATCH, HKV, D, generator=g) * 0.5
-    q = torch.randn(BATCH, HQ, D, generator=g) * 0.5
+    k = torch.randn(T, HKV, D, generator=g) * 0.5
+    q = torch.randn(T, HQ, D, generator=g) * 0.5
     ref.append_kv(0, k, k, meta)
     ref.attend(q, 0, 0.125, meta)  # warm-up
     times = []
@@ -129,157 +326,323 @@ def cpu_baseline(lens, budget_s=12.0):
     times.sort()
     layer_s = times[len(times) // 2]
     step_s = layer_s * LAYERS
-    return {"value": round(BATCH / step_s, 2), "unit": "decode tok/s", "cores": cores,
+    return {"value": round(T / step_s, 2), "unit": "decode tok/s", "cores": cores,
             "kind": "port",
-            "sample": (f"{len(times)} single-layer append+attend passes over all {BATCH} "
+            "sample": (f"{len(times)} single-layer append+attend passes over all {T} "
                        f"sequences (fp32, CPU restatement of PagedTorchBackend), median "
                        f"{layer_s * 1e3:.1f} ms/layer x {LAYERS} layers")}
+
+
+# ---------------------------------------------------------------- capacity ---
+
+def bench_capacity(args):
+    import torch
+    # ~200 GB pool: 381 469 blocks of 512 KiB (16 layers x K,V x 16 KiB)
+    nb = int(200e9 // (LAYERS * 2 * BS * HKV * D * 2))
+    rng = random.Random(SEED)
+    phase_a = [rng.randint(16, 64) for _ in range(4096)]
+    phase_b = lognormal_lengths(512, 2048)
+    out = {}
+    for name, lens in (("A", phase_a), ("B", phase_b)):
+        r = run_decode_like(args, lens, nb, f"capacity phase {name}")
+        out[name] = {"sequences": len(lens), "mean_len": round(sum(lens) / len(lens), 1),
+                     "tokens": sum(lens), "pages": r["pages"], "ms_per_step": round(r["ms"], 4),
+                     "GB/s": round(r["gbps"], 1),
+                     "pct_peak_hbm": round(100 * r["gbps"] / PEAK_HBM_GBPS, 2),
+                     "decode_tok_s": round(r["tok_s"], 1),
+                     "launch_ms": round(r["launch_ms"], 5),
+                     "eager_ms_per_step": round(r["eager"]["ms_per_step"], 4)}
+        del r
+        torch.cuda.empty_cache()
+    total_bytes = sum(LAYERS * decode_bytes(l, sum(-(-n // BS) for n in l))
+                      for l in (phase_a, phase_b))
+    total_ms = out["A"]["ms_per_step"] + out["B"]["ms_per_step"]
+    gbps = total_bytes / (total_ms * 1e-3) / 1e9
+    line = base_line(
+        args, "capacity decode attn+append HBM GB/s (% peak), 1 GPU", round(gbps, 1), "GB/s",
+        total_ms, "fp16",
+        (f"capacity decode: phase A 4096 seqs uniform[16,64], phase B 512 seqs lognormal "
+         f"mean 2048 clipped 2048; {GEOM}; pool {nb} blocks (~200 GB), shuffled tables"),
+        layers=LAYERS, pool_blocks=nb, part_pages=args.part_pages)
+    line.update({"pct_peak_hbm": round(100 * gbps / PEAK_HBM_GBPS, 2), "phases": out,
+                 "roofline": {"bound": "hbm", "achieved": round(gbps, 1),
+                              "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                              "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None}})
+    return line
+
+
+# ----------------------------------------------------------------- prefill ---
+
+def bench_prefill(args):
+    import torch
+    from llm_serving_layer_amd import ScheduledSeq, SequenceBlocks, build_batch_meta
+    from llm_serving_layer_amd.backend import MI355XBackend
+
+    n_seq, prefix, chunk = 8, 1536, 512
+    nb = 2 * (prefix // BS + n_seq * chunk // BS)
+    device = "cuda:0"
+    bk = MI355XBackend(LAYERS, nb, BS, HKV, HQ, D, device=device, dtype=torch.float16)
+    fill_pool(bk, SEED)
+    alloc = shuffled_allocator(nb)
+    pre = SequenceBlocks(alloc, seq_id=1000)
+    pre.append(prefix)                      # the radix-cached prefix, 96 full blocks
+    seqs = []
+    for i in range(n_seq):
+        s = SequenceBlocks(alloc, seq_id=i)
+        alloc.incref(pre.block_ids)
+        s.block_ids = list(pre.block_ids)
+        s.num_tokens = prefix
+        s.append(chunk)
+        seqs.append(s)
+    meta = build_batch_meta([ScheduledSeq(s, [0] * chunk) for s in seqs], device, BS)
+    T = n_seq * chunk
+    g = torch.Generator(device=device).manual_seed(SEED + 2)
+    k = (torch.randn(LAYERS, T, HKV, D, generator=g, device=device) * 0.5).half()
+    v = (torch.randn(LAYERS, T, HKV, D, generator=g, device=device) * 0.5).half()
+    q = (torch.randn(LAYERS, T, HQ, D, generator=g, device=device) * 0.5).half()
+
+    def step(events):
+        for l in range(LAYERS):
+            bk.append_kv(l, k[l], v[l], meta)
+            if events is not None:
+                events[l][0].record()
+            bk.attend(q[l], l, 0.125, meta)
+            if events is not None:
+                events[l][1].record()
+
+    log(f"prefill: {n_seq} x ({prefix} shared + {chunk}) tokens, q_tile {bk.q_tile}")
+    eager = time_eager(step, args.steps, args.warmup, LAYERS)
+    bk.check_device_errors()
+    # masked-exact flops: 4 d per visible (query, key) pair and query head
+    pairs = sum(prefix + j + 1 for j in range(chunk))
+    layer_flops = 4 * D * pairs * HQ * n_seq
+    attend_ms = eager["launch_ms"]
+    tflops = layer_flops / (attend_ms * 1e-3) / 1e12
+    ms = eager["ms_per_step"]
+    step_tflops = LAYERS * layer_flops / (ms * 1e-3) / 1e12
+    line = base_line(
+        args, "chunked-prefill attention TFLOP/s over a shared paged prefix, 1 GPU",
+        round(step_tflops, 2), "TFLOP/s", ms, "fp16",
+        (f"chunked prefill: 8 seqs share a 1536-token paged prefix, each appends a 512-token "
+         f"chunk (causal in the chunk), 16 layers x (KV append + attention); {GEOM}"),
+        layers=LAYERS, q_tile=bk.q_tile)
+    line.update({
+        "flops_per_layer": layer_flops,
+        "roofline": {"kernel": "pkv::prefill_kernel<_Float16,64,4>", "bound": "mfma",
+                     "achieved": round(tflops, 2), "peak": PEAK_MFMA_F16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_MFMA_F16_TFLOPS, 4),
+                     "traffic": traffic_for("prefill_kernel_config4"),
+                     "avg_launch_ms": round(attend_ms, 5),
+                     "timing": "HIP events around each attend launch"},
+        "eager": {k2: round(v2, 4) for k2, v2 in eager.items()},
+    })
+    return line
+
+
+# -------------------------------------------------------------------- copy ---
+
+def bench_copy(args):
+    import torch
+    from llm_serving_layer_amd import _native
+    from llm_serving_layer_amd.backend import MI355XBackend
+
+    pairs, nb, shared = 4096, 16384, 64
+    device = "cuda:0"
+    bk = MI355XBackend(LAYERS, nb, BS, HKV, HQ, D, device=device, dtype=torch.float16)
+    fill_pool(bk, SEED)
+    rng = random.Random(SEED)
+    perm = list(range(nb))
+    rng.shuffle(perm)
+    prefix_set = perm[:shared]                    # shared-prefix blocks, sources repeat
+    uniq = perm[shared:shared + pairs]
+    dsts = perm[shared + pairs:shared + 2 * pairs]
+    srcs = [rng.choice(prefix_set) if rng.random() < 0.27 else uniq[i] for i in range(pairs)]
+    n_shared = sum(1 for s in srcs if s in set(prefix_set))
+    ids = torch.tensor(srcs + dsts, dtype=torch.int32, device=device)
+    lib = bk._lib
+
+    def launch(events):
+        if events is not None:
+            events[0][0].record()
+        rc = lib.pkv_copy_blocks(bk._pool.data_ptr(), LAYERS, bk._plane_bytes, bk._block_bytes,
+                                 nb, ids.data_ptr(), ids.data_ptr() + 4 * pairs, pairs,
+                                 bk._status.data_ptr(),
+                                 torch.cuda.current_stream().cuda_stream)
+        _native.check(rc, "copy_blocks")
+        if events is not None:
+            events[0][1].record()
+
+    log(f"copy: {pairs} pairs ({n_shared} from {shared} shared-prefix blocks)")
+    eager = time_eager(launch, args.steps, args.warmup, 1)
+    bk.check_device_errors()
+    # the public API (host validation + id upload) for comparison
+    t0 = time.perf_counter()
+    for _ in range(3):
+        bk.copy_blocks(srcs, dsts)
+    torch.cuda.synchronize()
+    api_ms = (time.perf_counter() - t0) * 1e3 / 3
+    step_bytes = 2 * pairs * LAYERS * 2 * bk._block_bytes + 8 * pairs
+    ms = eager["launch_ms"]
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    line = base_line(
+        args, "copy-on-write block copy HBM GB/s (% peak), 1 GPU", round(gbps, 1), "GB/s",
+        eager["ms_per_step"], "fp16",
+        (f"radix copy-on-write: {pairs} block pairs per step, 27% of sources from a "
+         f"{shared}-block shared prefix, 16 layers x K,V x 16 KiB per block"),
+        pairs=pairs, pool_blocks=nb, shared_sources=n_shared)
+    line.update({
+        "pct_peak_hbm": round(100 * gbps / PEAK_HBM_GBPS, 2),
+        "copies_per_s": round(pairs / (ms * 1e-3), 1),
+        "public_api_ms_per_step": round(api_ms, 3),
+        "roofline": {"kernel": "pkv::block_kernel (copy)", "bound": "hbm",
+                     "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "traffic": traffic_for("block_copy_config3a"),
+                     "avg_launch_ms": round(ms, 5)},
+    })
+    return line
+
+
+# -------------------------------------------------------------------- swap ---
+
+def bench_swap(args):
+    import torch
+    from llm_serving_layer_amd import SequenceBlocks
+    from llm_serving_layer_amd.backend import MI355XBackend
+    from llm_serving_layer_amd.swap import KVSwapSpace
+
+    n_seq, toks = 64, 256
+    nb = 4 * n_seq * toks // BS
+    device = "cuda:0"
+    bk = MI355XBackend(LAYERS, nb, BS, HKV, HQ, D, device=device, dtype=torch.float16)
+    fill_pool(bk, SEED)
+    alloc = shuffled_allocator(nb)
+    space = KVSwapSpace(bk)
+    seqs = []
+    for i in range(n_seq):
+        s = SequenceBlocks(alloc, seq_id=i)
+        s.append(toks)
+        seqs.append(s)
+    nbytes = space.bytes_for(n_seq * toks // BS)
+
+    # the host link itself: one pinned copy of the same size each way
+    dev = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    for _ in range(2):
+        host.copy_(dev, non_blocking=True)
+        dev.copy_(host, non_blocking=True)
+    torch.cuda.synchronize()
+    link = {}
+    for name, (dst, src) in (("d2h", (host, dev)), ("h2d", (dev, host))):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(3):
+            dst.copy_(src, non_blocking=True)
+        b.record()
+        torch.cuda.synchronize()
+        link[name] = nbytes * 3 / (a.elapsed_time(b) * 1e-3) / 1e9
+    del dev, host
+
+    log(f"swap: {n_seq} x {toks} tokens, {nbytes / 2**20:.0f} MiB each way")
+    outs, ins = [], []
+    for it in range(args.warmup + args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        handles = [space.swap_out(f"r{i}", s) for i, s in enumerate(seqs)]
+        space.synchronize()
+        t1 = time.perf_counter()
+        fresh = []
+        for s in seqs:
+            s.free()
+        for i in range(n_seq):
+            s = SequenceBlocks(alloc, seq_id=i)
+            s.append(toks)
+            fresh.append(s)
+        t2 = time.perf_counter()
+        for h, s in zip(handles, fresh):
+            space.swap_in(h, s)
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        for h in handles:
+            space.release(h)
+        seqs = fresh
+        if it >= args.warmup:
+            outs.append(t1 - t0)
+            ins.append(t3 - t2)
+    bk.check_device_errors()
+    out_s, in_s = sorted(outs)[len(outs) // 2], sorted(ins)[len(ins) // 2]
+    out_gbps, in_gbps = nbytes / out_s / 1e9, nbytes / in_s / 1e9
+    both = 2 * nbytes / (out_s + in_s) / 1e9
+    line = base_line(
+        args, "preemption swap GB/s per direction over the host link, 1 GPU", round(both, 2),
+        "GB/s", (out_s + in_s) * 1e3, "fp16",
+        (f"preemption swap: {n_seq} sequences x {toks} tokens (1024 blocks, 512 MiB) out to "
+         f"pinned host memory and back into different blocks; {GEOM}"),
+        sequences=n_seq, tokens_each=toks)
+    line.update({
+        "swap_out_GB/s": round(out_gbps, 2), "swap_in_GB/s": round(in_gbps, 2),
+        "roofline": {"bound": "host link", "achieved": round(both, 2),
+                     "peak": round(min(link.values()), 2), "unit": "GB/s",
+                     "frac": round(both / min(link.values()), 4), "traffic": None,
+                     "peak_source": "pinned copy of the same size in this run",
+                     "link_d2h_GB/s": round(link["d2h"], 2),
+                     "link_h2d_GB/s": round(link["h2d"], 2)},
+    })
+    return line
+
+
+# ------------------------------------------------------------- calibration ---
+
+def bench_calib(args):
+    """A plain device-to-device copy of 1 GiB: the known-size reference that
+    scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+    n = 1 << 30
+    x = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    y = torch.empty_like(x)
+    x.fill_(1)
+    for _ in range(args.warmup):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(args.steps):
+        y.copy_(x)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    gbps = 2 * n / (ms * 1e-3) / 1e9
+    line = base_line(args, "device copy HBM GB/s (calibration)", round(gbps, 1), "GB/s", ms,
+                     "u8", "1 GiB device-to-device copy (reads 1 GiB, writes 1 GiB)", bytes=n)
+    line["roofline"] = {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
+                        "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None}
+    return line
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--part-pages", type=int, default=4)
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "prefill", "copy", "swap", "capacity", "calib"])
+    ap.add_argument("--part-pages", type=int, default=None,
+                    help="split-K partition size in pages (default: the backend's)")
+    ap.add_argument("--eager", action="store_true",
+                    help="decode: report the call-by-call step, no graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--graph", action="store_true",
-                    help="also time the step captured in a HIP graph and replayed")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path has no cross-GPU exchange (each GPU "
               f"serves its own sequences); --gpus {args.gpus} is not supported.", file=sys.stderr)
         return 2
-
-    import torch
-
-    device = "cuda:0"
-    lens = lengths()
-    print(f"[bench] building workload: batch {BATCH}, {sum(lens)} tokens", file=sys.stderr, flush=True)
-    bk, meta, k, v, q, pages, meta_ms = build(device, lens, args.part_pages)
-    dec_bytes, app_bytes = algorithmic_bytes(lens, pages, BATCH)
-    step_bytes = LAYERS * (dec_bytes + app_bytes)
-    scale = 1.0 / 8.0
-
-    def step(events=None):
-        for l in range(LAYERS):
-            bk.append_kv(l, k[l], v[l], meta)
-            if events is not None:
-                events[l][0].record()
-            bk.attend(q[l], l, scale, meta)
-            if events is not None:
-                events[l][1].record()
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    bk.check_device_errors()
-
-    # Timed region: K steps through the public API, bracketed by syncs.
-    print(f"[bench] timing {args.steps} steps", file=sys.stderr, flush=True)
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(LAYERS)] for _ in range(args.steps)]
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record()
-    for s in range(args.steps):
-        step(ev[s])
-    stop.record()
-    enqueue_s = time.perf_counter() - t0   # host time to issue every call (no sync yet)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = start.elapsed_time(stop)
-    ms_per_step = max(gpu_ms, wall * 1e3) / args.steps
-    attend_ms = [ev[s][l][0].elapsed_time(ev[s][l][1]) for s in range(args.steps)
-                 for l in range(LAYERS)]
-    attend_avg_ms = sum(attend_ms) / len(attend_ms)
-    bk.check_device_errors()
-
-    graph = None
-    if args.graph:
-        # The same step captured once into a HIP graph and replayed: removes the
-        # host's per-call cost; the kernels and their order are unchanged.
-        print("[bench] graph capture", file=sys.stderr, flush=True)
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            step()
-        torch.cuda.current_stream().wait_stream(side)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            step()
-        for _ in range(args.warmup):
-            g.replay()
-        torch.cuda.synchronize()
-        gs, ge = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        gs.record()
-        for _ in range(args.steps):
-            g.replay()
-        ge.record()
-        torch.cuda.synchronize()
-        g_ms = gs.elapsed_time(ge) / args.steps
-        graph = {"ms_per_step": round(g_ms, 4),
-                 "GB/s": round(step_bytes / (g_ms * 1e-3) / 1e9, 1),
-                 "decode_tok_s": round(BATCH / (g_ms * 1e-3), 1)}
-        bk.check_device_errors()
-
-    gbps = step_bytes / (ms_per_step * 1e-3) / 1e9
-    dec_gbps = dec_bytes / (attend_avg_ms * 1e-3) / 1e9
-    cpu = None
-    if not args.no_cpu_baseline:
-        print("[bench] CPU baseline (oracle)", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(lens, args.cpu_budget)
-    traffic = None
-    tfile = ROOT / "profiles" / "decode_kernel_traffic_config2.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-
-    line = {
-        "metric": METRIC,
-        "value": round(gbps, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic",
-        "config": {
-            "workload": ("paged decode step: 16 layers x (KV append + paged decode attention), "
-                         "batch 256, Llama-3.2-1B attention geometry 32q/8kv/d64, block 16, "
-                         "lognormal context lengths mean 258 (seed 20260731)"),
-            "batch": BATCH, "layers": LAYERS, "context_tokens": sum(lens), "pages": pages,
-            "pool_blocks": 2 * pages, "part_pages": args.part_pages,
-        },
-        "pct_peak_hbm": round(100 * gbps / PEAK_HBM_GBPS, 2),
-        "decode_tok_s": round(BATCH / (ms_per_step * 1e-3), 1),
-        "algorithmic_bytes_per_step": step_bytes,
-        "metadata_build_upload_ms": round(meta_ms, 3),
-        "timing": {"gpu_ms_per_step": round(gpu_ms / args.steps, 4),
-                   "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
-                   "host_enqueue_ms_per_step": round(enqueue_s * 1e3 / args.steps, 4)},
-        "roofline": {
-            "kernel": "decode_kernel (+ merge_kernel for split sequences), per layer",
-            "bound": "hbm",
-            "achieved": round(dec_gbps, 1),
-            "peak": PEAK_HBM_GBPS,
-            "unit": "GB/s",
-            "frac": round(dec_gbps / PEAK_HBM_GBPS, 4),
-            "traffic": traffic,
-            "algorithmic_bytes_per_launch": dec_bytes,
-            "avg_launch_ms": round(attend_avg_ms, 5),
-        },
-        "cpu_baseline": cpu,
-        "graph_replay": graph,
-    }
-    if cpu:
-        line["gpu_over_cpu"] = round(line["decode_tok_s"] / cpu["value"], 1)
-    print(json.dumps(line))
+    if args.part_pages is None:
+        from llm_serving_layer_amd.backend import DEFAULT_PART_PAGES
+        args.part_pages = DEFAULT_PART_PAGES
+    fn = {"decode": bench_decode, "prefill": bench_prefill, "copy": bench_copy,
+          "swap": bench_swap, "capacity": bench_capacity, "calib": bench_calib}[args.workload]
+    print(json.dumps(fn(args)))
     return 0
 
 
