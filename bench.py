@@ -268,7 +268,7 @@ def bench_decode(args):
             "kernel": "pkv::decode_kernel<_Float16,64,4,1> (KV append fused), one launch per layer",
             "bound": "hbm", "achieved": round(r["kern_gbps"], 1), "peak": PEAK_HBM_GBPS,
             "unit": "GB/s", "frac": round(r["kern_gbps"] / PEAK_HBM_GBPS, 4),
-            "traffic": traffic_for("decode_kernel_config2"),
+            "traffic": traffic_for("decode_kernel_batch256"),
             "algorithmic_bytes_per_launch": r["layer_bytes"],
             "avg_launch_ms": round(r["launch_ms"], 5),
             "timing": ("graph replay time / 16 launches, HIP events on the replay stream"
@@ -431,7 +431,7 @@ def bench_prefill(args):
         "roofline": {"kernel": "pkv::prefill_kernel<_Float16,64,4>", "bound": "mfma",
                      "achieved": round(tflops, 2), "peak": PEAK_MFMA_F16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_MFMA_F16_TFLOPS, 4),
-                     "traffic": traffic_for("prefill_kernel_config4"),
+                     "traffic": traffic_for("prefill_kernel_8x512"),
                      "avg_launch_ms": round(attend_ms, 5),
                      "timing": "HIP events around each attend launch"},
         "eager": {k2: round(v2, 4) for k2, v2 in eager.items()},
@@ -497,7 +497,7 @@ def bench_copy(args):
         "roofline": {"kernel": "pkv::block_kernel (copy)", "bound": "hbm",
                      "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(gbps / PEAK_HBM_GBPS, 4),
-                     "traffic": traffic_for("block_copy_config3a"),
+                     "traffic": traffic_for("block_copy_4096_pairs"),
                      "avg_launch_ms": round(ms, 5)},
     })
     return line
