@@ -4,16 +4,19 @@
 // pages are cut into partitions of at most part_pages pages (split-K over
 // the KV axis; the split depends only on that sequence's own length, so its
 // result never depends on what it is batched with). One workgroup owns one
-// partition for every KV head: one wave per KV head (two heads per wave
-// beyond 8 KV heads).
+// partition for a group of up to 4 KV heads: one wave per KV head (two heads
+// per wave beyond 8 KV heads in a group).
 //
 // Memory: a page is 16 token rows x (all KV heads x head_dim) contiguous in
-// the pool. The workgroup reads it as whole rows -- lane chunk k is bytes
-// [16 (tid + k * threads), +16) of the page -- so each wave instruction
-// covers consecutive 128-byte lines, the pattern that streams fastest. The
-// pages arrive in registers two pages ahead of use, are copied to one of two
+// the pool; a head group's slice of a row is 512 contiguous bytes at the
+// headline geometry. The workgroup reads its slice of every row whole --
+// lane chunk k is bytes [16 c, +16) of the slice sequence, c = tid + k *
+// threads -- so each wave instruction covers whole 128-byte lines. The pages
+// arrive in registers two pages ahead of use, are copied to one of two
 // padded LDS page buffers, and one barrier per page separates filling a
-// buffer from reading it.
+// buffer from reading it. Small workgroups (4 waves) keep four resident per
+// compute unit, so one workgroup's start and end latencies overlap others'
+// streaming.
 //
 // Per wave, head and page (G query heads share the KV head, G <= 16):
 //  1. S^T = K Q^T with one 16x16x32 MFMA per 32 dims: the K rows (from LDS)
@@ -56,6 +59,7 @@ namespace pkv {
 //  n_partitions of the sequence, first slot of the sequence}
 constexpr int kWorkInts = 8;
 constexpr int kMaxWaves = 8;      // waves per workgroup (one per KV head), at most
+constexpr int kGroupHeads = 4;    // KV heads per workgroup (its slice of each page row)
 constexpr int kMaxPartPages = 64; // a partition's page ids fit one wave-wide load
 
 // Layout of one partition's partial output: per (slot, KV head), NGR groups
@@ -216,14 +220,19 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int NW = blockDim.x >> 6;
-  const int rowb = n_kv_heads * D * (int)sizeof(T);  // bytes per token row, all heads
+  const int HGW = NW * HPW;                          // KV heads of this workgroup
+  const int n_groups = n_kv_heads / HGW;
+  const int wi = blockIdx.x / n_groups;              // partition
+  const int hg = blockIdx.x - wi * n_groups;         // head group: heads hg*HGW ..
+  const int frow = n_kv_heads * D * (int)sizeof(T);  // bytes per token row, all heads
+  const int rowb = HGW * D * (int)sizeof(T);         // bytes of the group's slice of a row
   const int RS = rowb + 16;                          // padded LDS row stride
   // Two page buffers, each [16][RS] K rows then [16][RS] V rows.
   constexpr int kBufs = 2;
   // past both the page tiles and the merge scratch (see decode_lds_bytes)
   int* s_flag = reinterpret_cast<int*>(smem + max(kBufs * 2 * PS * RS, NW * 64 * 4 * NGR * 4));
 
-  const int32_t* w = work + kWorkInts * blockIdx.x;
+  const int32_t* w = work + kWorkInts * wi;
   const int seq = w[0], pbase = w[1], npp = w[2], slot = w[3];
   const int kv_len = w[4], tok0 = w[5], nparts = w[6], slot0 = w[7];
   const int Hq = n_kv_heads * G;
@@ -246,10 +255,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   for (int k = 0; k < CPL; ++k) {
     const int c = tid + k * NW * 64;
     lrow[k] = c / cpr;
-    goff[k] = (uint32_t)c * 16;
+    goff[k] = (uint32_t)(lrow[k] * frow + hg * rowb + (c - lrow[k] * cpr) * 16);
     loff[k] = (uint32_t)(lrow[k] * RS + (c - lrow[k] * cpr) * 16);
   }
-  const uint32_t page_bytes = (uint32_t)(PS * rowb);
+  const uint32_t page_bytes = (uint32_t)(PS * frow);
   auto load_page = [&](int j, vec8* kr, vec8* vr) {
     const int64_t page = __builtin_amdgcn_readlane(pid, j);
     const __amdgpu_buffer_rsrc_t rk = ws_rsrc(kpool + page * PS * row, page_bytes);
@@ -268,7 +277,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   vec8 qb[HPW][NCH];
 #pragma unroll
   for (int hh = 0; hh < HPW; ++hh) {
-    const int h = wave + hh * NW;
+    const int h = hg * HGW + wave + hh * NW;
     const T* qr = q + ((int64_t)seq * Hq + h * G + (n < G ? n : 0)) * D + g * 8;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -297,7 +306,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
 #pragma unroll
       for (int k = 0; k < CPL; ++k) {
         if (lrow[k] == tl) {
-          const uint32_t col = goff[k] - (uint32_t)tl * rowb;
+          const uint32_t col = goff[k] - (uint32_t)tl * frow;
           *reinterpret_cast<vec8*>(kd + col) = *reinterpret_cast<const vec8*>(kn + col);
           *reinterpret_cast<vec8*>(vd + col) = *reinterpret_cast<const vec8*>(vn + col);
         }
@@ -328,7 +337,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
 #pragma unroll
       for (int k = 0; k < CPL; ++k) {
         if (lrow[k] == tl) {
-          const uint32_t col = goff[k] - (uint32_t)tl * rowb;
+          const uint32_t col = goff[k] - (uint32_t)tl * frow;
           kr[k] = *reinterpret_cast<const vec8*>(kn + col);
           vr[k] = *reinterpret_cast<const vec8*>(vn + col);
         }
@@ -348,7 +357,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     const int tp = tok0 + j * PS;
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
-      const int h = wave + hh * NW;
+      const int h = wave + hh * NW;  // the head's column in the group's LDS rows
       // S^T: lane (n, g) gets the scores of tokens 4g..4g+3 for head n.
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       const unsigned char* kp = kl + n * RS + (h * D + g * 8) * (int)sizeof(T);
@@ -416,7 +425,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   if (slot < 0) {
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
-      const int h = wave + hh * NW;
+      const int h = hg * HGW + wave + hh * NW;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * g + i;
@@ -436,7 +445,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   const __amdgpu_buffer_rsrc_t rm = ws_rsrc(part_ml, ml_bytes);
 #pragma unroll
   for (int hh = 0; hh < HPW; ++hh) {
-    const int h = wave + hh * NW;
+    const int h = hg * HGW + wave + hh * NW;
     const uint32_t head_off = (uint32_t)(((int64_t)slot * n_kv_heads + h) * PL::FLOATS * 4);
     if (g < NGR) {
 #pragma unroll
@@ -453,7 +462,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   // before the workgroup counts its arrival.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  int32_t* cnt = counters + seq;
+  int32_t* cnt = counters + (int64_t)seq * n_groups + hg;
   if (tid == 0)
     *s_flag = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
@@ -464,7 +473,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   float* wts = reinterpret_cast<float*>(smem) + wave * 64 * (4 * NGR);
 #pragma unroll
   for (int hh = 0; hh < HPW; ++hh)
-    merge_head<T, D, G>(out, wts, seq, wave + hh * NW, n_kv_heads, nparts, slot0, ro, rm);
+    merge_head<T, D, G>(out, wts, seq, hg * HGW + wave + hh * NW, n_kv_heads, nparts, slot0,
+                        ro, rm);
   if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -482,9 +492,10 @@ static void launch(const void* q, void* out, void* kp, void* vp, int64_t nb,
                    float sl2, const void* kn, const void* vn, const int32_t* slots, float* po,
                    float* pml, uint32_t o_bytes, uint32_t ml_bytes, int32_t* cnt,
                    int32_t* status, hipStream_t s) {
-  const int nw = Hkv / HPW;
-  hipLaunchKernelGGL((decode_kernel<T, D, G, HPW>), dim3((unsigned)n_work), dim3(nw * 64),
-                     decode_lds_bytes(Hkv, D, G), s, (const T*)q, (T*)out, (T*)kp, (T*)vp, nb,
+  const int hgw = std::min<int>(Hkv, kGroupHeads);  // KV heads per workgroup
+  const int nw = hgw / HPW;
+  hipLaunchKernelGGL((decode_kernel<T, D, G, HPW>), dim3((unsigned)(n_work * (Hkv / hgw))),
+                     dim3(nw * 64), decode_lds_bytes(hgw, D, G), s, (const T*)q, (T*)out, (T*)kp, (T*)vp, nb,
                      indices, work, Hkv, sl2, (const T*)kn, (const T*)vn, slots, po, pml, o_bytes,
                      ml_bytes, cnt, status);
 }
@@ -506,14 +517,19 @@ static LaunchFn pick_g(int G) {
   }
 }
 
-// Heads per wave: the workgroup has one wave per KV head up to kMaxWaves.
-static int heads_per_wave(int Hkv) { return Hkv <= kMaxWaves ? 1 : Hkv / kMaxWaves; }
+// Heads per wave: the workgroup has one wave per KV head of its group, up to
+// kMaxWaves.
+static int heads_per_wave(int Hkv) {
+  const int hgw = std::min(Hkv, kGroupHeads);
+  return hgw <= kMaxWaves ? 1 : hgw / kMaxWaves;
+}
 
 template <typename T>
 static LaunchFn pick(int Hkv, int D, int G) {
   // Whole-row staging needs rows of at most 2 KiB and Hkv a power of two up
   // to 2 * kMaxWaves (so that waves x heads per wave covers every head).
-  if (Hkv < 1 || Hkv > 2 * kMaxWaves || (Hkv & (Hkv - 1)) || Hkv * D * 2 > 2048) return nullptr;
+  const int hgw = std::min(Hkv, kGroupHeads);
+  if (Hkv < 1 || (Hkv & (Hkv - 1)) || hgw > 2 * kMaxWaves || hgw * D * 2 > 2048) return nullptr;
   const int hpw = heads_per_wave(Hkv);
   switch (D) {
     case 64: return hpw == 1 ? pick_g<T, 64, 1>(G) : pick_g<T, 64, 2>(G);
