@@ -52,7 +52,7 @@ __all__ = ["MI355XBackend", "is_available", "unavailable_reason"]
 _DTYPES = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16,
            torch.float32: _native.DTYPE_F32}
 
-DEFAULT_PART_PAGES = 8   # split-K partition: 8 pages = 128 tokens per wave
+DEFAULT_PART_PAGES = 10  # split-K partition: 10 pages = 160 tokens
 MAX_PART_PAGES = 64      # a partition's page ids are read by one wavefront
 DEFAULT_Q_TILE = 64      # prefill tile when the geometry has no matrix-core kernel
 
@@ -442,13 +442,14 @@ class MI355XBackend:
         ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
         n_work, n_slots = C.c_int32(), C.c_int32()
         if not use_prefill:
-            cap = 8 * (int(indptr[-1]) + n)
+            cap = 2 + 9 * (int(indptr[-1]) + n) + 1
             buf = np.empty(cap, dtype=np.int32)
+            plan_len = C.c_int32()
             rc = self._lib.pkv_plan_decode(ptr(indptr32), ptr(kvl32), ptr(last32), n,
                                            self.block_size, self.part_pages, ptr(buf), cap,
-                                           C.byref(n_work), C.byref(n_slots))
+                                           C.byref(plan_len), C.byref(n_work), C.byref(n_slots))
             _native.check(rc, "plan (decode)")
-            used = 8 * n_work.value
+            used = plan_len.value
             need = self._lib.pkv_decode_workspace_bytes(n, n_slots.value, self.n_heads,
                                                         self.n_kv_heads, self.head_dim)
             if need > self._workspace.numel():
