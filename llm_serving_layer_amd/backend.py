@@ -442,14 +442,13 @@ class MI355XBackend:
         ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
         n_work, n_slots = C.c_int32(), C.c_int32()
         if not use_prefill:
-            cap = 2 + 9 * (int(indptr[-1]) + n) + 1
+            cap = 8 * (int(indptr[-1]) + n)
             buf = np.empty(cap, dtype=np.int32)
-            plan_len = C.c_int32()
             rc = self._lib.pkv_plan_decode(ptr(indptr32), ptr(kvl32), ptr(last32), n,
                                            self.block_size, self.part_pages, ptr(buf), cap,
-                                           C.byref(plan_len), C.byref(n_work), C.byref(n_slots))
+                                           C.byref(n_work), C.byref(n_slots))
             _native.check(rc, "plan (decode)")
-            used = plan_len.value
+            used = 8 * n_work.value
             need = self._lib.pkv_decode_workspace_bytes(n, n_slots.value, self.n_heads,
                                                         self.n_kv_heads, self.head_dim)
             if need > self._workspace.numel():
