@@ -156,3 +156,40 @@ def test_error_codes_map_to_reference_exception_types():
     with pytest.raises(ValueError):
         _native.check(rc, "copy")
     assert lib.pkv_last_error()
+
+
+def _host_backend(part_pages=10):
+    """The backend's host half (planning) over the real library, with CPU
+    tensors standing in for device ones: exercises every host call the
+    launch path makes, with the binding table's signatures."""
+    bk = object.__new__(MI355XBackend)
+    bk._lib = _native.load()
+    bk.device = torch.device("cpu")
+    bk.num_layers, bk.num_blocks, bk.block_size = 1, 64, 16
+    bk.n_kv_heads, bk.n_heads, bk.head_dim = 8, 32, 64
+    bk.part_pages = part_pages
+    bk.q_tile = bk._lib.pkv_prefill_q_tile(32, 8, 64, 16, _native.DTYPE_F16)
+    bk._workspace = torch.zeros(0, dtype=torch.uint8)
+    bk._planned, bk._slot_cache, bk._pending = None, None, None
+    bk.n_plans = bk.n_runs = 0
+    return bk
+
+
+def test_backend_plans_decode_and_prefill_through_the_library():
+    from llm_serving_layer_amd import BlockAllocator, SequenceBlocks
+
+    from ._util import grow_and_assemble
+
+    bk = _host_backend(part_pages=2)
+    alloc = BlockAllocator(64, 16)
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(3)]
+    pre = grow_and_assemble(seqs, [40, 100, 7], 16)
+    p = bk._ensure_planned(pre)
+    assert p.use_prefill and p.n_work > 0 and p.plan.numel() == 4 * p.n_work
+    assert bk._ensure_planned(pre) is p and bk.n_plans == 1, "planned once per meta"
+    dec = grow_and_assemble(seqs, [1, 1, 1], 16)
+    p = bk._ensure_planned(dec)
+    assert not p.use_prefill and p.fusable and p.n_slots > 0
+    assert p.plan.numel() == 8 * p.n_work
+    assert bk._workspace.numel() >= bk._lib.pkv_decode_workspace_bytes(
+        3, p.n_slots, 32, 8, 64)
