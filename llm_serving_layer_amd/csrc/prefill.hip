@@ -27,9 +27,14 @@
 namespace pkv {
 
 constexpr int kPrefillRows = 128;  // query rows per workgroup (tokens x heads)
+// One 16-row block per wave: 8 waves per workgroup at 108 VGPRs keep four
+// waves per SIMD, which hides the score/softmax VALU work better than two
+// row blocks per wave at half the waves.
+constexpr int kPrefillRB = 1;
+constexpr int kPrefillThreads = kPrefillRows / 16 / kPrefillRB * 64;
 
 template <typename T, int D, int G>
-__global__ __launch_bounds__(256) void prefill_kernel(
+__global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
     const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kpool,
     const T* __restrict__ vpool, int64_t num_blocks, const int32_t* __restrict__ cu_q,
     const int32_t* __restrict__ kv_indptr, const int32_t* __restrict__ kv_indices,
@@ -42,11 +47,12 @@ __global__ __launch_bounds__(256) void prefill_kernel(
   constexpr int NPG = TT / PS;           // pages per KV tile
   constexpr int NCH = D / 32;            // QK k-chunks
   constexpr int NDB = D / 16;            // PV dim blocks
-  constexpr int RB = 2;                  // 16-row blocks per wave
+  constexpr int RB = kPrefillRB;         // 16-row blocks per wave
+  constexpr int NT = kPrefillThreads;
   constexpr int RSB = D * (int)sizeof(T) + 16;  // padded LDS row bytes
   constexpr int CPR = D * (int)sizeof(T) / 16;  // 16-byte chunks per head row
-  constexpr int CPT = TT * CPR / 256;           // chunks per thread per tensor per tile
-  static_assert(CPT >= 1 && TT * CPR % 256 == 0, "tile must split evenly over 256 threads");
+  constexpr int CPT = TT * CPR / NT;            // chunks per thread per tensor per tile
+  static_assert(CPT >= 1 && TT * CPR % NT == 0, "tile must split evenly over the threads");
   // [buffer][K, V][TT rows of RSB bytes]
   extern __shared__ __align__(16) unsigned char lds_raw[];
   auto lds_tile = [&](int buf, int kv) { return lds_raw + (buf * 2 + kv) * TT * RSB; };
@@ -89,7 +95,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(
   auto load_tile = [&](int t, vec8* kr, vec8* vr) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int c = tid + 256 * k;
+      const int c = tid + NT * k;
       const int tok = t * TT + c / CPR;
       kr[k] = vec8{};
       vr[k] = vec8{};
@@ -111,7 +117,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(
     unsigned char* vl = lds_tile(t & 1, 1);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int c = tid + 256 * k;
+      const int c = tid + NT * k;
       const int off = (c / CPR) * RSB + (c % CPR) * 16;
       *reinterpret_cast<vec8*>(kl + off) = kr[k];
       *reinterpret_cast<vec8*>(vl + off) = vr[k];
@@ -132,6 +138,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(
     const unsigned char* kl = lds_tile(t & 1, 0);
     const unsigned char* vl = lds_tile(t & 1, 1);
     const int t0 = t * TT;
+    const bool full = t0 + TT - 1 <= base_pos;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       float sc[NPG][4];
@@ -145,8 +152,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(
           acc = Mma<T>::qk(*reinterpret_cast<const vec8*>(kp + c * 64), qb[rb][c], acc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          // keys past the row's position (hence past kv_len) are masked
-          const bool live = t0 + jj * PS + 4 * g + i <= qpos[rb];
+          // keys past the row's position (hence past kv_len) are masked;
+          // a tile that ends at or before the first query's position needs none
+          const bool live = full || t0 + jj * PS + 4 * g + i <= qpos[rb];
           sc[jj][i] = live ? acc[i] * scale_log2 : -INFINITY;
           mx = fmaxf(mx, sc[jj][i]);
         }
@@ -239,7 +247,7 @@ static void launch_prefill(const void* q, void* out, const void* kp, const void*
                            int32_t Hkv, float sl2, int32_t* status, hipStream_t s) {
   constexpr int TT = D <= 64 ? 64 : 32;
   const size_t lds = 2 * 2 * TT * (D * sizeof(T) + 16);  // two K+V tiles of TT padded rows
-  hipLaunchKernelGGL((prefill_kernel<T, D, G>), dim3((unsigned)(n_tiles * Hkv)), dim3(256), lds,
+  hipLaunchKernelGGL((prefill_kernel<T, D, G>), dim3((unsigned)(n_tiles * Hkv)), dim3(kPrefillThreads), lds,
                      s, (const T*)q, (T*)out, (const T*)kp, (const T*)vp, nb, cu_q, indptr,
                      indices, kv_lens, plan, Hkv, sl2, status);
 }
