@@ -3,35 +3,55 @@
 // One workgroup (4 waves) owns one KV head h and one tile of a sequence's
 // query rows: 128 rows = BQ query tokens x G query heads (BQ = 128 / G), so
 // every K/V tile it loads serves all G query heads of the KV head. Each wave
-// owns two blocks of 16 rows. Query row r of the tile is token r / G (of the
-// tile) and query head h*G + r % G; it sits at absolute position
-// kv_len - q_len + token (bottom-right causal alignment, as the reference's
+// owns 32 rows. Query row r of the tile is token r / G (of the tile) and
+// query head h*G + r % G; it sits at absolute position kv_len - q_len +
+// token (bottom-right causal alignment, as the reference's
 // triu(diagonal = kv_len - q_len + 1) mask) and sees keys 0..position.
 //
-// The KV axis is walked 64 tokens (4 pages; 32 for head_dim 128) at a time.
-// A tile of K and of V (those rows x head_dim of head h) is loaded two tiles
-// ahead into registers, staged in one of two padded LDS buffers, and read by
-// every wave:
-//  * S^T = K Q^T: 16x16x32 MFMA, K rows from LDS as the A operand, Q^T held
-//    in registers as the B operand; lane (row n, group g) gets the scores of
-//    tokens 4g..4g+3 of each page for its query row n;
-//  * online softmax per query row (two cross-lane steps per max / sum);
-//  * O += P V: 16x16x32 MFMA over two pages at a time. The probabilities a
-//    lane holds for pages 2k and 2k+1 are its A operand as they are (the
-//    contraction index runs over those 8 tokens in that order); the V B
-//    operand is the matching pair of transposing LDS reads.
+// The KV axis is walked 32 tokens (two pages) at a time. A tile of K and of
+// V (those rows x head_dim of head h) is loaded two tiles ahead into
+// registers, staged in one of two padded LDS buffers, and read by every
+// wave. All products are 32x32x16 MFMAs, so every LDS byte read feeds 32
+// query rows:
+//  * S^T = K Q^T: K rows from LDS as the A operand, Q^T held in registers
+//    as the B operand. Lane (row n, group g) gets 16 scores of its query row
+//    n: keys 8 i + 4 g + 0..3, i = 0..3;
+//  * online softmax per query row, lane-local but for one cross-lane step
+//    per max / sum;
+//  * O^T = V^T P^T: V^T from transposing LDS reads as the A operand, the
+//    lane's own 8 probabilities of a 16-key block as the B operand (the
+//    contraction index runs over keys 4 g + 0..3, 8 + 4 g + 0..3 of the
+//    block). Every O^T accumulator of a lane belongs to its own query row,
+//    so rescaling needs no cross-lane traffic.
+// The running max moves lazily: only when a row's max grows by more than
+// 2^8 (in exp2 units) are the accumulators rescaled, so probabilities stay
+// at most 256 and o / l is unchanged. Tiles wholly below the causal
+// diagonal skip the mask. Each wave's share of a tile lies within one page,
+// so page ids are scalar reads and pages are buffer ranges: rows past
+// kv_len read zeros without a memory access.
 // Numerics as serving/backends/paged_torch.py:443-485: scores, softmax and
 // accumulation in fp32; probabilities rounded to the pool dtype before PV.
+// The scale must be positive (the row max is taken before scaling); other
+// scales run the generic kernel.
 #include "mfma.h"
 
 namespace pkv {
 
-constexpr int kPrefillRows = 128;  // query rows per workgroup (tokens x heads)
-// One 16-row block per wave: 8 waves per workgroup at 108 VGPRs keep four
-// waves per SIMD, which hides the score/softmax VALU work better than two
-// row blocks per wave at half the waves.
-constexpr int kPrefillRB = 1;
-constexpr int kPrefillThreads = kPrefillRows / 16 / kPrefillRB * 64;
+constexpr int kPrefillRows = 128;   // query rows per workgroup (tokens x heads)
+constexpr int kPrefillThreads = 256; // 4 waves x 32 rows
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+template <typename T> struct Mma32;
+template <> struct Mma32<_Float16> {
+  __device__ static f32x16 mma(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mma32<__bf16> {
+  __device__ static f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
@@ -41,26 +61,24 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
     const int32_t* __restrict__ kv_lens, const int32_t* __restrict__ plan,
     int32_t n_kv_heads, float scale_log2, int32_t* status) {
   typedef typename Mma<T>::vec8 vec8;
-  constexpr int BQ = kPrefillRows / G;   // query tokens per tile
-  constexpr int TT = D <= 64 ? 64 : 32;  // KV tokens per tile (LDS stays under 64 KiB)
+  typedef typename Mma<T>::vec4 vec4;
+  constexpr int TT = 32;                 // KV tokens per tile
   constexpr int PS = 16;
-  constexpr int NPG = TT / PS;           // pages per KV tile
-  constexpr int NCH = D / 32;            // QK k-chunks
-  constexpr int NDB = D / 16;            // PV dim blocks
-  constexpr int RB = kPrefillRB;         // 16-row blocks per wave
+  constexpr int NH = TT / 32;            // 32-key halves per tile
+  constexpr int NC = D / 16;             // QK k-chunks of 16 dims
+  constexpr int NDH = D / 32;            // PV blocks of 32 dims
   constexpr int NT = kPrefillThreads;
-  constexpr int RSB = D * (int)sizeof(T) + 16;  // padded LDS row bytes
-  constexpr int CPR = D * (int)sizeof(T) / 16;  // 16-byte chunks per head row
-  constexpr int CPT = TT * CPR / NT;            // chunks per thread per tensor per tile
+  constexpr int RSB = D * (int)sizeof(T) + 16;
+  constexpr int CPR = D * (int)sizeof(T) / 16;
+  constexpr int CPT = TT * CPR / NT;
   static_assert(CPT >= 1 && TT * CPR % NT == 0, "tile must split evenly over the threads");
-  // [buffer][K, V][TT rows of RSB bytes]
   extern __shared__ __align__(16) unsigned char lds_raw[];
   auto lds_tile = [&](int buf, int kv) { return lds_raw + (buf * 2 + kv) * TT * RSB; };
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int n = lane & 15, g = lane >> 4;
+  const int n = lane & 31, g = lane >> 5;
   const int item = blockIdx.x / n_kv_heads;
   const int h = blockIdx.x - item * n_kv_heads;
   const int seq = plan[4 * item], qs = plan[4 * item + 1], qn = plan[4 * item + 2];
@@ -70,48 +88,53 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
   const int pbase = kv_indptr[seq];
   const int Hq = n_kv_heads * G;
   const int64_t row = (int64_t)n_kv_heads * D;
-  const int base_pos = kv_len - q_len + qs;  // position of the tile's first query token
-  const int kv_end = base_pos + qn;          // keys [0, kv_end) are visible to some row
+  const int base_pos = kv_len - q_len + qs;
+  const int kv_end = base_pos + qn;
   const int ntiles = (kv_end + TT - 1) / TT;
 
-  // Per row block: Q^T (B operand), this lane's query row position.
-  vec8 qb[RB][NCH];
-  int qpos[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int r = (wave * RB + rb) * 16 + n;
-    const int tok = r / G;
-    const bool valid = tok < qn;
-    // padding rows see every key so their running max stays finite
-    qpos[rb] = valid ? base_pos + tok : kv_len - 1;
+  // This lane's query row (column n of every 32x32 tile) and Q^T as the B
+  // operand of S^T = K Q^T: lane (n, g) holds Q[row][16c + 8g .. + 7].
+  const int r = wave * 32 + n;
+  const int tok = r / G;
+  const bool valid = tok < qn;
+  const int qpos = valid ? base_pos + tok : kv_len - 1;
+  vec8 qb[NC];
+  {
     const T* qr = q + ((int64_t)(q0 + qs + (valid ? tok : 0)) * Hq + h * G + r % G) * D + g * 8;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const vec8 t = *reinterpret_cast<const vec8*>(qr + c * 32);
-      qb[rb][c] = valid ? t : vec8{};
+    for (int c = 0; c < NC; ++c) {
+      const vec8 t = *reinterpret_cast<const vec8*>(qr + c * 16);
+      qb[c] = valid ? t : vec8{};
     }
   }
 
+  // Each wave's share of a tile lies in one page (its lanes cover 64 x 16
+  // bytes of consecutive rows of a page), so the page id is a scalar read
+  // and the page a buffer range: rows at or past kv_len and tiles past the
+  // end read zeros without touching memory, and every tile issues the same
+  // loads (exact wait counts in the pipelined loop).
+  const int npages = (kv_len + PS - 1) / PS;
+  const uint32_t rowbytes = (uint32_t)(row * sizeof(T));
   auto load_tile = [&](int t, vec8* kr, vec8* vr) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int c = tid + NT * k;
-      const int tok = t * TT + c / CPR;
-      kr[k] = vec8{};
-      vr[k] = vec8{};
-      if (tok < kv_len) {
-        int pid = kv_indices[pbase + tok / PS];
-        if (pid < 0 || (int64_t)pid >= num_blocks) {
-          flag(status, PKV_STATUS_BAD_PAGE);
-          pid = 0;
-        }
-        const int64_t off = ((int64_t)pid * PS + tok % PS) * row + (int64_t)h * D + (c % CPR) * 8;
-        kr[k] = *reinterpret_cast<const vec8*>(kpool + off);
-        vr[k] = *reinterpret_cast<const vec8*>(vpool + off);
-      }
+      const int tk0 = t * TT + __builtin_amdgcn_readfirstlane((wave * 64 + NT * k) / CPR);
+      const int pg = tk0 / PS;
+      const int live_rows = min(PS, kv_len - pg * PS);   // <= 0 past the end
+      const int raw = kv_indices[pbase + min(pg, npages - 1)];
+      const bool bad = raw < 0 || (int64_t)raw >= num_blocks;
+      if (bad && lane == 0) flag(status, PKV_STATUS_BAD_PAGE);
+      const int pid = __builtin_amdgcn_readfirstlane(bad ? 0 : raw);
+      const __amdgpu_buffer_rsrc_t rk = ws_rsrc(const_cast<T*>(kpool) + (int64_t)pid * PS * row,
+                                                live_rows > 0 ? live_rows * rowbytes : 0);
+      const __amdgpu_buffer_rsrc_t rv = ws_rsrc(const_cast<T*>(vpool) + (int64_t)pid * PS * row,
+                                                live_rows > 0 ? live_rows * rowbytes : 0);
+      const uint32_t off = (uint32_t)(((c / CPR) % PS) * rowbytes + (h * D + (c % CPR) * 8) * sizeof(T));
+      kr[k] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+      vr[k] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
     }
   };
-  // Rows past kv_len were loaded as zeros, so V can never carry stale bits.
   auto stage = [&](int t, const vec8* kr, const vec8* vr) {
     unsigned char* kl = lds_tile(t & 1, 0);
     unsigned char* vl = lds_tile(t & 1, 1);
@@ -124,117 +147,126 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
     }
   };
 
-  f32x4 o[RB][NDB];
-  float m_run[RB], l_run[RB];
+  // O^T accumulators: o[dh][rr] = O[row][32 dh + 8 (rr / 4) + 4 g + rr % 4].
+  f32x16 o[NDH];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    m_run[rb] = -INFINITY;
-    l_run[rb] = 0.f;
-#pragma unroll
-    for (int b = 0; b < NDB; ++b) o[rb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int dh = 0; dh < NDH; ++dh) o[dh] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.f;
+  // the transposing V reads: lane i of each 16-lane block points at key
+  // (i / 4) of a 4-key group and dims 4 (i % 4) .. + 3 of its 16-dim block
+  const int vrow = lane & 15;
+  const int vcol = (lane & 16) + 4 * (vrow & 3);
 
   auto compute = [&](int t) {
     const unsigned char* kl = lds_tile(t & 1, 0);
     const unsigned char* vl = lds_tile(t & 1, 1);
     const int t0 = t * TT;
     const bool full = t0 + TT - 1 <= base_pos;
+    // S^T = K Q^T: s[hf][rr] = score of key t0 + 32 hf + 8 (rr / 4) + 4 g + rr % 4.
+    f32x16 s[NH];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      float sc[NPG][4];
-      float mx = -INFINITY;
+    for (int hf = 0; hf < NH; ++hf) {
+      s[hf] = f32x16{};
+      const unsigned char* kp = kl + (hf * 32 + n) * RSB + g * 16;
 #pragma unroll
-      for (int jj = 0; jj < NPG; ++jj) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const unsigned char* kp = kl + (jj * PS + n) * RSB + g * 16;
+      for (int c = 0; c < NC; ++c)
+        s[hf] = Mma32<T>::mma(*reinterpret_cast<const vec8*>(kp + c * 32), qb[c], s[hf]);
+    }
+    // Raw-score row max (scale_log2 > 0, so scaling commutes with max);
+    // keys past the row's position are masked only on tiles that reach them.
+    if (!full) {
 #pragma unroll
-        for (int c = 0; c < NCH; ++c)
-          acc = Mma<T>::qk(*reinterpret_cast<const vec8*>(kp + c * 64), qb[rb][c], acc);
+      for (int hf = 0; hf < NH; ++hf) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          // keys past the row's position (hence past kv_len) are masked;
-          // a tile that ends at or before the first query's position needs none
-          const bool live = full || t0 + jj * PS + 4 * g + i <= qpos[rb];
-          sc[jj][i] = live ? acc[i] * scale_log2 : -INFINITY;
-          mx = fmaxf(mx, sc[jj][i]);
+        for (int rr = 0; rr < 16; ++rr) {
+          const int key = t0 + 32 * hf + 8 * (rr >> 2) + 4 * g + (rr & 3);
+          if (key > qpos) s[hf][rr] = -INFINITY;
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // finite: key 0 is visible to every row, and tiles run from key 0 up
-      const float m_new = fmaxf(m_run[rb], mx);
-      const float alpha = __builtin_amdgcn_exp2f(m_run[rb] - m_new);
-      vec8 pk[NPG / 2];
-      float ls = 0.f;
+    }
+    float mx = -INFINITY;
 #pragma unroll
-      for (int jj = 0; jj < NPG; ++jj) {
+    for (int hf = 0; hf < NH; ++hf) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = __builtin_amdgcn_exp2f(sc[jj][i] - m_new);
-          ls += e;
-          pk[jj / 2][(jj & 1) * 4 + i] = (T)e;
-        }
+      for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, s[hf][rr]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+    // Lazy rescale: the reference max only moves when a row's max grows by
+    // more than 2^8 (then p <= 256, exact in the pool dtype's range); the
+    // result o / l does not depend on which reference is used.
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f)) {
+      const float m_new = fmaxf(m_run, mx);   // finite: key 0 is visible to every row
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int dh = 0; dh < NDH; ++dh) o[dh] *= alpha;
+    }
+    // P^T as the B operand of O^T = V^T P^T: 16-key block (hf, qq) uses
+    // the lane's scores rr = 8 qq .. 8 qq + 7 in that order.
+    vec8 pb[NH * 2];
+    float ls = 0.f;
+#pragma unroll
+    for (int hf = 0; hf < NH; ++hf) {
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hf][rr], scale_log2, -m_run));
+        ls += e;
+        pb[2 * hf + (rr >> 3)][rr & 7] = (T)e;
       }
-      ls += __shfl_xor(ls, 16, 64);
-      ls += __shfl_xor(ls, 32, 64);
-      l_run[rb] = l_run[rb] * alpha + ls;
-      m_run[rb] = m_new;
+    }
+    ls += __shfl_xor(ls, 32, 64);
+    l_run += ls;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a = __shfl(alpha, 4 * g + i, 64);
+    for (int kb = 0; kb < NH * 2; ++kb) {
+      // V^T as the A operand: lane (dim, g) holds V[key][dim] for keys
+      // 16 kb + 4 g + 0..3 and 16 kb + 8 + 4 g + 0..3.
+      const unsigned char* vp = vl + (16 * kb + 4 * g + (vrow >> 2)) * RSB + vcol * (int)sizeof(T);
 #pragma unroll
-        for (int b = 0; b < NDB; ++b) o[rb][b][i] *= a;
-      }
-#pragma unroll
-      for (int kk = 0; kk < NPG / 2; ++kk) {
-        const unsigned char* v0 =
-            vl + (2 * kk * PS + 4 * g + (n >> 2)) * RSB + 4 * (n & 3) * (int)sizeof(T);
-        const unsigned char* v1 = v0 + PS * RSB;
-#pragma unroll
-        for (int b = 0; b < NDB; ++b) {
-          const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_i16x4*)(v0 + 16 * b * sizeof(T)));
-          const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_i16x4*)(v1 + 16 * b * sizeof(T)));
-          const vec8 vb = __builtin_bit_cast(
-              vec8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          o[rb][b] = Mma<T>::qk(pk[kk], vb, o[rb][b]);
-        }
+      for (int dh = 0; dh < NDH; ++dh) {
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(vp + 32 * dh * sizeof(T)));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(vp + 8 * RSB + 32 * dh * sizeof(T)));
+        const vec8 va = __builtin_bit_cast(
+            vec8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[dh] = Mma32<T>::mma(va, pb[kb], o[dh]);
       }
     }
   };
 
   vec8 kA[CPT], vA[CPT], kB[CPT], vB[CPT];
   load_tile(0, kA, vA);
-  if (ntiles > 1) load_tile(1, kB, vB);
+  load_tile(1, kB, vB);
   stage(0, kA, vA);
-  if (ntiles > 2) load_tile(2, kA, vA);
+  load_tile(2, kA, vA);
   __syncthreads();
-  for (int t = 0; t < ntiles; t += 2) {  // two register sets, so unrolled by two
+  // two register sets, so unrolled by two; re-entered only after the
+  // second half, so both halves' loads are in flight there
+  for (int t = 0;; t += 2) {
     if (t + 1 < ntiles) stage(t + 1, kB, vB);
-    if (t + 3 < ntiles) load_tile(t + 3, kB, vB);
+    load_tile(t + 3, kB, vB);
     compute(t);
     __syncthreads();
-    if (t + 1 < ntiles) {
-      if (t + 2 < ntiles) stage(t + 2, kA, vA);
-      if (t + 4 < ntiles) load_tile(t + 4, kA, vA);
-      compute(t + 1);
-      __syncthreads();
-    }
+    if (t + 1 >= ntiles) break;
+    if (t + 2 < ntiles) stage(t + 2, kA, vA);
+    load_tile(t + 4, kA, vA);
+    compute(t + 1);
+    __syncthreads();
+    if (t + 2 >= ntiles) break;
   }
 
-  // lane (dim column n, group g) holds rows 4g+i of each block, dims 16b + n.
+  if (valid) {
+    const float inv = 1.f / l_run;
+    T* orow = out + ((int64_t)(q0 + qs + tok) * Hq + h * G + r % G) * D + 4 * g;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
+    for (int dh = 0; dh < NDH; ++dh) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = (wave * RB + rb) * 16 + 4 * g + i;
-      const int tok = r / G;
-      const float li = __shfl(l_run[rb], 4 * g + i, 64);  // lane 4g+i holds row 4g+i's sum
-      if (tok < qn) {
-        T* orow = out + ((int64_t)(q0 + qs + tok) * Hq + h * G + r % G) * D + n;
+      for (int j = 0; j < 4; ++j) {
+        vec4 v;
 #pragma unroll
-        for (int b = 0; b < NDB; ++b) orow[16 * b] = (T)(o[rb][b][i] / li);
+        for (int e = 0; e < 4; ++e) v[e] = (T)(o[dh][4 * j + e] * inv);
+        *reinterpret_cast<vec4*>(orow + 32 * dh + 8 * j) = v;
       }
     }
   }
@@ -245,7 +277,7 @@ static void launch_prefill(const void* q, void* out, const void* kp, const void*
                            const int32_t* cu_q, const int32_t* indptr, const int32_t* indices,
                            const int32_t* kv_lens, const int32_t* plan, int32_t n_tiles,
                            int32_t Hkv, float sl2, int32_t* status, hipStream_t s) {
-  constexpr int TT = D <= 64 ? 64 : 32;
+  constexpr int TT = 32;
   const size_t lds = 2 * 2 * TT * (D * sizeof(T) + 16);  // two K+V tiles of TT padded rows
   hipLaunchKernelGGL((prefill_kernel<T, D, G>), dim3((unsigned)(n_tiles * Hkv)), dim3(kPrefillThreads), lds,
                      s, (const T*)q, (T*)out, (const T*)kp, (const T*)vp, nb, cu_q, indptr,
@@ -305,7 +337,8 @@ int run_fast_prefill(const void* q, void* out, const void* kp, const void* vp, i
                      bool* ran) {
   *ran = false;
   PrefillFn fn = fast_prefill(dtype, Hq, Hkv, D, page_size);
-  if (!fn || !plan || n_tiles <= 0 || q_tile != kPrefillRows / (Hq / Hkv)) return PKV_OK;
+  if (!fn || !plan || n_tiles <= 0 || q_tile != kPrefillRows / (Hq / Hkv) || !(scale > 0.f))
+    return PKV_OK;
   if ((int64_t)n_tiles * Hkv > 0x7fffffffLL) return fail(PKV_ERR_INVALID, "too many tiles");
   if (((uintptr_t)q | (uintptr_t)kp | (uintptr_t)vp) % 16)
     return fail(PKV_ERR_INVALID, "q and pools must be 16-byte aligned");

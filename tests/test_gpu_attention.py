@@ -183,6 +183,18 @@ def test_matrix_core_prefill_matches_generic_kernel(dtype):
     assert diff <= (4e-3 if dtype == torch.float16 else 3.2e-2), diff
 
 
+def test_prefill_with_a_negative_scale_matches_the_oracle():
+    """The matrix-core prefill takes the row max before scaling, so it
+    declines a non-positive scale; the generic kernel then serves the same
+    plan. Either way the result is the oracle's."""
+    print("prefill, negative scale", flush=True)
+    p = Pair(1, 64, 16, 8, 32, 64)
+    alloc = BlockAllocator(64, 16)
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(2)]
+    res = p.step(grow_and_assemble(seqs, [70, 33], 16), 21, scale=-0.125)
+    check(res, "negative scale")
+
+
 def test_config1_fp16_fast_path_and_fp32_fixture():
     """The CPU plumbing case on the GPU: fp32 pools vs the golden float64
     outputs, fp16 pools (fast decode kernel) vs the fp32 oracle."""
