@@ -26,7 +26,8 @@
 //  2. online softmax in registers: mask past kv_len, running max / sum with
 //     two cross-lane steps; p = 2^(s*scale*log2e - m) rounded to the pool
 //     dtype -- four values per lane that are exactly the A operand of a
-//     16x16x16 MFMA;
+//     16x16x16 MFMA. The reference max m moves lazily (only when a head's
+//     max grows by more than 2^8), so most pages skip the rescale of o;
 //  3. PV on MFMA: ds_read_b64_tr_b16 hands each lane 4 consecutive tokens of
 //     one V dim, the B operand, one read per 16 dims. V rows past kv_len are
 //     zeroed in LDS so stale bits can never reach the sum.
@@ -373,27 +374,32 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[hh], mx);  // finite: every page has a live token
-      const float alpha = __builtin_amdgcn_exp2f(m_run[hh] - m_new);
+      // Lazy rescale: the reference max moves only when some head's max
+      // grows by more than 2^8, so p <= 256 and o / l is unchanged.
+      if (__builtin_amdgcn_ballot_w64(mx > m_run[hh] + 8.f)) {
+        const float m_new = fmaxf(m_run[hh], mx);  // finite: every page has a live token
+        const float alpha = __builtin_amdgcn_exp2f(m_run[hh] - m_new);
+        l_run[hh] *= alpha;
+        m_run[hh] = m_new;
+        // lane (n, g) holds output rows 4g+i, whose factor lives in lane 4g+i
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+          for (int b = 0; b < NDB; ++b) o[hh][b][i] *= a;
+        }
+      }
       vec4 p;
       float ls = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float e = __builtin_amdgcn_exp2f(sc[i] - m_new);
+        const float e = __builtin_amdgcn_exp2f(sc[i] - m_run[hh]);
         ls += e;
         p[i] = (T)e;
       }
       ls += __shfl_xor(ls, 16, 64);
       ls += __shfl_xor(ls, 32, 64);
-      l_run[hh] = l_run[hh] * alpha + ls;
-      m_run[hh] = m_new;
-      // lane (n, g) holds output rows 4g+i, whose factor lives in lane 4g+i
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a = __shfl(alpha, 4 * g + i, 64);
-#pragma unroll
-        for (int b = 0; b < NDB; ++b) o[hh][b][i] *= a;
-      }
+      l_run[hh] += ls;
       const unsigned char* vp =
           vl + (4 * g + (n >> 2)) * RS + (h * D + 4 * (n & 3)) * (int)sizeof(T);
 #pragma unroll
