@@ -44,6 +44,8 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
@@ -182,12 +184,17 @@ def decode_setup(device, lens, nb, part_pages):
         s = SequenceBlocks(alloc, seq_id=i)
         s.append(n - 1)          # history; the step appends the n-th token
         seqs.append(s)
-    t0 = time.perf_counter()
     for s in seqs:
         s.append(1)
-    meta = build_batch_meta([ScheduledSeq(s, [0]) for s in seqs], device, BS)
-    torch.cuda.synchronize()
-    meta_ms = (time.perf_counter() - t0) * 1e3
+    # steady-state host cost of one step's metadata: build + upload, the
+    # median of several builds after a first (warm-up) one
+    times = []
+    for _ in range(8):
+        t0 = time.perf_counter()
+        meta = build_batch_meta([ScheduledSeq(s, [0]) for s in seqs], device, BS)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    meta_ms = float(np.median(times[1:]))
     T = len(lens)
     g = torch.Generator(device=device).manual_seed(SEED + 1)
     k = (torch.randn(LAYERS, T, HKV, D, generator=g, device=device) * 0.5).half()
@@ -221,13 +228,18 @@ def run_decode_like(args, lens, nb, label):
         log("graph capture + replay")
         graph, _g = time_graph(step, args.steps, args.warmup)
         bk.check_device_errors()
-    # plan + metadata end to end: dropping the plan forces a re-plan
-    t0 = time.perf_counter()
-    bk.invalidate_plan()
-    bk.attend(torch.zeros(len(lens), HQ, D, dtype=torch.float16, device="cuda:0"), 0, 0.125,
-              meta)
-    torch.cuda.synchronize()
-    plan_ms = (time.perf_counter() - t0) * 1e3
+    # planning (one device-to-host copy + the host plan + its upload), median
+    # of several: dropping the plan forces a re-plan on the next attend
+    qz = torch.zeros(len(lens), HQ, D, dtype=torch.float16, device="cuda:0")
+    times = []
+    for _ in range(6):
+        bk.invalidate_plan()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        bk.attend(qz, 0, 0.125, meta)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    plan_ms = float(np.median(times[1:]))
     run = graph or eager
     ms = run["ms_per_step"]
     launch_ms = ms / LAYERS if graph else eager["launch_ms"]

@@ -17,12 +17,13 @@ device=...)`` calls are ten synchronous H2D round trips per step.
 from __future__ import annotations
 
 from dataclasses import dataclass, field
+from itertools import chain
 
 import numpy as np
 import torch
 
-from .contract import BatchMeta
-from .paging import SequenceBlocks, build_csr
+from .contract import BatchMeta, validate_host
+from .paging import SequenceBlocks
 
 __all__ = ["ScheduledSeq", "build_batch_meta", "build_token_tensor"]
 
@@ -84,38 +85,50 @@ def build_batch_meta(seqs: list[ScheduledSeq], device, page_size: int,
     if page_size <= 0:
         raise ValueError(f"page_size must be positive, got {page_size}")
 
+    # Per-sequence scalars in one pass each; the index arrays below are built
+    # with array operations from them and the concatenated page lists.
     n = len(seqs)
-    qlens = np.empty(n, dtype=np.int64)
-    kvlens = np.empty(n, dtype=np.int64)
-    for i, s in enumerate(seqs):
-        _check_seq(i, s)
-        if s.blocks.block_size != page_size:
-            raise ValueError(f"seq {i} (seq_id={s.blocks.seq_id}) has block_size="
-                             f"{s.blocks.block_size} but the batch declares "
-                             f"page_size={page_size}")
-        qlens[i] = s.query_len
-        kvlens[i] = s.kv_len
+    blocks = [s.blocks for s in seqs]
+    qlens = np.fromiter((len(s.new_token_ids) for s in seqs), np.int64, n)
+    kvlens = np.fromiter((b.num_tokens for b in blocks), np.int64, n)
+    nblk = np.fromiter((len(b.block_ids) for b in blocks), np.int64, n)
+    bsz = np.fromiter((b.block_size for b in blocks), np.int64, n)
+    freed = np.fromiter((b.is_freed for b in blocks), bool, n)
+    bad = freed | (qlens <= 0) | (qlens > kvlens) | (kvlens > nblk * bsz) | (bsz != page_size)
+    if bad.any():  # the first offender raises the per-sequence message
+        i = int(np.argmax(bad))
+        _check_seq(i, seqs[i])
+        raise ValueError(f"seq {i} (seq_id={blocks[i].seq_id}) has block_size="
+                         f"{blocks[i].block_size} but the batch declares "
+                         f"page_size={page_size}")
 
     cu = np.zeros(n + 1, dtype=np.int64)
     np.cumsum(qlens, out=cu[1:])
     T = int(cu[-1])
-    positions = np.concatenate([np.arange(k - q, k) for q, k in zip(qlens, kvlens)])
     batch_idx = np.repeat(np.arange(n), qlens)
-    slots = np.fromiter((sl for s in seqs for sl in s.blocks.slots_for_new_tokens(s.query_len)),
-                        dtype=np.int64, count=T)
-    indptr, indices, last = build_csr([s.blocks for s in seqs])
+    # absolute positions kv_len - q .. kv_len - 1 of each sequence's tokens
+    positions = np.arange(T, dtype=np.int64) + (kvlens - qlens - cu[:-1])[batch_idx]
+    indptr = np.zeros(n + 1, dtype=np.int64)
+    np.cumsum(nblk, out=indptr[1:])
+    indices = np.fromiter(chain.from_iterable(b.block_ids for b in blocks), np.int64,
+                          int(indptr[-1]))
+    last = kvlens % page_size
+    last[last == 0] = page_size
+    # slot = block_ids[p // page_size] * page_size + p % page_size
+    slots = (indices[indptr[:-1][batch_idx] + positions // page_size] * page_size
+             + positions % page_size)
 
     parts = {
         "query_lens": qlens, "cu_query_lens": cu, "kv_lens": kvlens,
-        "last_token_ix": cu[1:] - 1, "kv_indptr": np.asarray(indptr, np.int64),
-        "kv_indices": np.asarray(indices, np.int64), "kv_last_page_len": np.asarray(last, np.int64),
+        "last_token_ix": cu[1:] - 1, "kv_indptr": indptr,
+        "kv_indices": indices, "kv_last_page_len": last,
         "batch_indices": batch_idx, "slot_mapping": slots,
     }
+    if validate:  # on the host arrays, before anything reaches the device
+        validate_host(n, page_size, qlens, cu, kvlens, indptr, last, cu[1:] - 1, positions,
+                      batch_idx, n_slots=T, n_pages=int(indices.shape[0]))
     fields = _upload(parts, positions, device, dtype_index)
-    meta = BatchMeta(**fields, page_size=page_size, is_prefill=bool((qlens > 1).any()))
-    if validate:
-        meta.validate()
-    return meta
+    return BatchMeta(**fields, page_size=page_size, is_prefill=bool((qlens > 1).any()))
 
 
 def _upload(parts: dict, positions: np.ndarray, device, dtype_index: torch.dtype) -> dict:

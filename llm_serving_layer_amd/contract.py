@@ -23,13 +23,10 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Optional, Protocol, runtime_checkable
 
+import numpy as np
 import torch
 
-__all__ = ["BatchMeta", "AttentionBackend"]
-
-
-def _host_list(t: torch.Tensor) -> list[int]:
-    return [int(x) for x in t.detach().to("cpu").reshape(-1).tolist()]
+__all__ = ["BatchMeta", "AttentionBackend", "validate_host"]
 
 
 @dataclass(frozen=True)
@@ -82,77 +79,110 @@ class BatchMeta:
         Assert every structural invariant whose violation would otherwise be
         silent (wrong pages read, a page dropped, a token routed to another
         sequence). Raises ``AssertionError``. Pulls the fields to the host
-        once; it is meant for batch assembly, not for the per-layer path.
+        in one transfer; it is meant for batch assembly, not for the
+        per-layer path.
         """
-        n = self.n_seqs
-        ps = int(self.page_size)
-        assert ps > 0, f"page_size must be positive, got {ps}"
-        assert n > 0, "BatchMeta describes no sequences"
+        names = ("query_lens", "cu_query_lens", "kv_lens", "kv_indptr", "kv_last_page_len",
+                 "last_token_ix", "positions", "batch_indices")
+        ts = [getattr(self, k).detach().reshape(-1) for k in names]
+        flat = torch.cat([t.to(torch.int64) for t in ts]).to("cpu").numpy()
+        parts, off = [], 0
+        for t in ts:
+            parts.append(flat[off:off + t.shape[0]])
+            off += t.shape[0]
+        n_slots = None if self.slot_mapping is None else int(self.slot_mapping.shape[0])
+        validate_host(self.n_seqs, int(self.page_size), *parts, n_slots=n_slots,
+                      n_pages=int(self.kv_indices.shape[0]))
 
-        ql = _host_list(self.query_lens)
-        cu = _host_list(self.cu_query_lens)
-        kv = _host_list(self.kv_lens)
-        indptr = _host_list(self.kv_indptr)
-        last = _host_list(self.kv_last_page_len)
-        ltok = _host_list(self.last_token_ix)
-        pos = _host_list(self.positions)
-        bidx = _host_list(self.batch_indices)
 
-        for name, vals in (("kv_lens", kv), ("kv_last_page_len", last),
-                           ("last_token_ix", ltok)):
-            assert len(vals) == n, f"{name} has {len(vals)} entries for {n} sequences"
-        assert len(cu) == n + 1, f"cu_query_lens has {len(cu)} entries, expected {n + 1}"
-        assert len(indptr) == n + 1, f"kv_indptr has {len(indptr)} entries, expected {n + 1}"
+def validate_host(n: int, ps: int, ql, cu, kv, indptr, last, ltok, pos, bidx, *,
+                  n_slots: Optional[int], n_pages: int) -> None:
+    """
+    BatchMeta's invariants over host int64 arrays. The common case (all
+    hold) is checked with array operations; on any violation the
+    sequence-by-sequence walk below reports the first one, in a fixed order.
+    """
+    ql, cu, kv, indptr, last, ltok, pos, bidx = (
+        np.asarray(x, dtype=np.int64) for x in (ql, cu, kv, indptr, last, ltok, pos, bidx))
+    ok = (ps > 0 and n > 0 and kv.shape[0] == n and last.shape[0] == n and ltok.shape[0] == n
+          and ql.shape[0] == n and cu.shape[0] == n + 1 and indptr.shape[0] == n + 1)
+    if ok:
+        tokens = int(cu[-1])
+        ok = (cu[0] == 0 and bool((np.diff(cu) == ql).all()) and pos.shape[0] == tokens
+              and bidx.shape[0] == tokens and (n_slots is None or n_slots == tokens)
+              and indptr[0] == 0 and indptr[-1] == n_pages)
+    if ok:
+        pages = np.diff(indptr)
+        ok = bool(((last >= 1) & (last <= ps) & (ql >= 1) & (ql <= kv)
+                   & (pages == (kv + ps - 1) // ps) & (kv - (pages - 1) * ps == last)
+                   & (ltok == cu[1:] - 1)).all())
+    if ok:
+        owner = np.repeat(np.arange(n, dtype=np.int64), ql)
+        ok = bool((bidx == owner).all()
+                  and (pos == np.arange(tokens, dtype=np.int64) + (kv - ql - cu[:-1])[owner]).all())
+    if not ok:
+        _walk(n, ps, [int(x) for x in ql], [int(x) for x in cu], [int(x) for x in kv],
+              [int(x) for x in indptr], [int(x) for x in last], [int(x) for x in ltok],
+              [int(x) for x in pos], [int(x) for x in bidx], n_slots, n_pages)
 
-        assert cu[0] == 0, f"cu_query_lens must start at 0, got {cu[0]}"
-        for i in range(n):
-            assert cu[i + 1] - cu[i] == ql[i], (
-                f"cu_query_lens {cu[i]}..{cu[i + 1]} disagrees with query_lens[{i}]={ql[i]}"
-            )
-        tokens = cu[-1]
-        assert len(pos) == tokens, f"positions has {len(pos)} entries for {tokens} tokens"
-        assert len(bidx) == tokens, (
-            f"batch_indices has {len(bidx)} entries for {tokens} tokens"
+
+def _walk(n, ps, ql, cu, kv, indptr, last, ltok, pos, bidx, n_slots, n_pages) -> None:
+    assert ps > 0, f"page_size must be positive, got {ps}"
+    assert n > 0, "BatchMeta describes no sequences"
+    for name, vals in (("kv_lens", kv), ("kv_last_page_len", last),
+                       ("last_token_ix", ltok), ("query_lens", ql)):
+        assert len(vals) == n, f"{name} has {len(vals)} entries for {n} sequences"
+    assert len(cu) == n + 1, f"cu_query_lens has {len(cu)} entries, expected {n + 1}"
+    assert len(indptr) == n + 1, f"kv_indptr has {len(indptr)} entries, expected {n + 1}"
+
+    assert cu[0] == 0, f"cu_query_lens must start at 0, got {cu[0]}"
+    for i in range(n):
+        assert cu[i + 1] - cu[i] == ql[i], (
+            f"cu_query_lens {cu[i]}..{cu[i + 1]} disagrees with query_lens[{i}]={ql[i]}"
         )
-        if self.slot_mapping is not None:
-            ns = int(self.slot_mapping.shape[0])
-            assert ns == tokens, f"slot_mapping has {ns} entries for {tokens} tokens"
+    tokens = cu[-1]
+    assert len(pos) == tokens, f"positions has {len(pos)} entries for {tokens} tokens"
+    assert len(bidx) == tokens, (
+        f"batch_indices has {len(bidx)} entries for {tokens} tokens"
+    )
+    if n_slots is not None:
+        assert n_slots == tokens, f"slot_mapping has {n_slots} entries for {tokens} tokens"
 
-        assert indptr[0] == 0, f"kv_indptr must start at 0, got {indptr[0]}"
-        n_pages_total = int(self.kv_indices.shape[0])
-        assert indptr[-1] == n_pages_total, (
-            f"kv_indptr ends at {indptr[-1]} but kv_indices holds {n_pages_total} pages"
+    assert indptr[0] == 0, f"kv_indptr must start at 0, got {indptr[0]}"
+    assert indptr[-1] == n_pages, (
+        f"kv_indptr ends at {indptr[-1]} but kv_indices holds {n_pages} pages"
+    )
+
+    for i in range(n):
+        assert 1 <= last[i] <= ps, (
+            f"seq {i}: kv_last_page_len={last[i]} outside [1, {ps}]; an exact "
+            f"multiple of page_size reports {ps}, never 0"
         )
-
-        for i in range(n):
-            assert 1 <= last[i] <= ps, (
-                f"seq {i}: kv_last_page_len={last[i]} outside [1, {ps}]; an exact "
-                f"multiple of page_size reports {ps}, never 0"
+        assert 1 <= ql[i] <= kv[i], (
+            f"seq {i}: query_len={ql[i]} must lie in [1, kv_len={kv[i]}]"
+        )
+        pages = indptr[i + 1] - indptr[i]
+        need = (kv[i] + ps - 1) // ps
+        assert pages == need, (
+            f"seq {i}: kv_len={kv[i]} needs {need} pages but {pages} pages allocated"
+        )
+        assert kv[i] - (pages - 1) * ps == last[i], (
+            f"seq {i}: kv_last_page_len={last[i]} but kv_len={kv[i]} over "
+            f"{pages} pages implies {kv[i] - (pages - 1) * ps}"
+        )
+        assert ltok[i] == cu[i + 1] - 1, (
+            f"seq {i}: last_token_ix={ltok[i]}, expected {cu[i + 1] - 1}"
+        )
+        for j in range(ql[i]):
+            t = cu[i] + j
+            assert bidx[t] == i, f"batch_indices[{t}]={bidx[t]}, expected {i}"
+            want = kv[i] - ql[i] + j
+            assert pos[t] == want, (
+                f"positions[{t}]={pos[t]}, expected absolute position {want}"
             )
-            assert 1 <= ql[i] <= kv[i], (
-                f"seq {i}: query_len={ql[i]} must lie in [1, kv_len={kv[i]}]"
-            )
-            pages = indptr[i + 1] - indptr[i]
-            need = (kv[i] + ps - 1) // ps
-            assert pages == need, (
-                f"seq {i}: kv_len={kv[i]} needs {need} pages but {pages} pages allocated"
-            )
-            assert kv[i] - (pages - 1) * ps == last[i], (
-                f"seq {i}: kv_last_page_len={last[i]} but kv_len={kv[i]} over "
-                f"{pages} pages implies {kv[i] - (pages - 1) * ps}"
-            )
-            assert ltok[i] == cu[i + 1] - 1, (
-                f"seq {i}: last_token_ix={ltok[i]}, expected {cu[i + 1] - 1}"
-            )
-            for j in range(ql[i]):
-                t = cu[i] + j
-                assert bidx[t] == i, f"batch_indices[{t}]={bidx[t]}, expected {i}"
-                want = kv[i] - ql[i] + j
-                assert pos[t] == want, (
-                    f"positions[{t}]={pos[t]}, expected absolute position {want}"
-                )
-        # is_prefill is a hint, not an invariant: backends that dispatch on it
-        # cross-check it against query_lens themselves and raise ValueError.
+    # is_prefill is a hint, not an invariant: backends that dispatch on it
+    # cross-check it against query_lens themselves and raise ValueError.
+    raise AssertionError("BatchMeta invariants disagree between checks")  # unreachable
 
 
 @runtime_checkable
