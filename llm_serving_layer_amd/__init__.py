@@ -8,7 +8,8 @@ hand-written gfx950 kernels (include/pagedkv.h, csrc/):
 * ``paging``    — BlockAllocator, SequenceBlocks, build_csr;
 * ``assembly``  — ScheduledSeq, build_batch_meta, build_token_tensor;
 * ``backend``   — MI355XBackend (append_kv / attend / copy_block[s]);
-* ``swap``      — KVSwapSpace / SwapHandle (preemption swap).
+* ``swap``      — KVSwapSpace / SwapHandle (preemption swap);
+* ``sizing``    — plan_kv_pool / KVPoolPlan (pool sizing for one MI355X).
 """
 
 from .assembly import ScheduledSeq, build_batch_meta, build_token_tensor
