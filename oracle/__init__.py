@@ -1,7 +1,7 @@
 """
 ORACLE — test infrastructure. CPU restatements of the reference's paged-KV
-path used only as the checker by tests/, ``__graft_entry__.smoke()`` and the
-CPU-baseline leg of bench.py. Nothing in llm_serving_layer_amd/ imports it.
+path, used only to check results in tests/ and ``__graft_entry__.smoke()``
+and as the timed CPU baseline in bench.py. Nothing in llm_serving_layer_amd/ imports it.
 """
 
 from .naive import (append_closed_form, copy_blocks_closed_form, gather_closed_form,

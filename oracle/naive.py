@@ -2,12 +2,12 @@
 ORACLE — test infrastructure, not product code (see oracle/paged_torch_cpu.py
 for who may import it).
 
-Independent checkers written in a style that shares nothing with the kernels
+Independent reference computations, written in a style that shares nothing with the kernels
 or with the op-for-op restatement:
 
 * ``naive_attention`` — textbook causal GQA attention on DENSE, unpaged K/V,
   explicit loops over heads and queries, float64, masking by not summing the
-  disallowed keys. Follows the reference's own independent checker,
+  disallowed keys. Follows the reference's own independent naive attention,
   tests/test_paged_torch.py:106-149 (query j may see keys
   [0, kv_len - q_len + j]; query head h reads KV head h // groups).
 * numpy closed forms for the pure data movement the reference performs with

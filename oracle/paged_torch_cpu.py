@@ -2,8 +2,8 @@
 ORACLE — test infrastructure, not product code.
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline leg may
-import this module, and only as the checker (or, for the baseline, as the
-timed CPU restatement). The product path never calls it.
+import this module, and only to check results against (or, for the
+baseline, as the timed CPU restatement). The product path never calls it.
 
 A CPU restatement of the reference's pure-PyTorch paged backend,
 serving/backends/paged_torch.py, op for op and at the same precisions:

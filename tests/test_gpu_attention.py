@@ -1,7 +1,7 @@
 """
 GPU parity of paged attention against the oracle.
 
-Bar (the north star's): fp16/bf16 output within max-abs 2e-3 / max-rel 1e-2
+Bar: fp16/bf16 output within max-abs 2e-3 / max-rel 1e-2
 of the oracle's fp32 computation on the same (fp16-rounded) inputs; fp32
 pools within 1e-5 of the float64 textbook. Structural known answers from the
 reference's tests/test_paged_torch.py (:303-649) and the differential harness
