@@ -82,6 +82,11 @@ int pkv_append_kv(void* k_pool, void* v_pool, int64_t num_slots,
  *    (-1: the partition is the whole sequence), kv_len, first token,
  *    n_partitions of the sequence, first slot of the sequence}
  * *n_slots_out: partial-result slots of split sequences (workspace size).
+ * When no sequence is split (*n_slots_out == 0), each partition is instead a
+ * pack of up to 16 whole consecutive sequences, at most `part_pages` pages
+ * together: {first seq, index of its first page in kv_indices, n_pages, -1,
+ * n_seqs in the pack, 0, 1, -1}. pkv_attend_decode reads a plan with
+ * n_slots == 0 as packs.
  */
 int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_lens,
                     const int32_t* kv_last_page_len, int32_t n_seqs,

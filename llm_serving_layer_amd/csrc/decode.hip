@@ -41,6 +41,17 @@
 // launch and an agent-scope release fence, whose L2 write-back walks the
 // whole cache.
 //
+// Packs: when no sequence of the batch is split, a partition holds up to 16
+// whole consecutive sequences (segments) whose pages follow each other in
+// kv_indices. The page pipeline runs straight through the pack; at each
+// segment's last page the wave writes that sequence's output, resets its
+// softmax state and switches to the next sequence's Q, loaded one segment
+// ahead. Per page and sequence the arithmetic is the same as in a partition
+// of its own, so results do not depend on the packing.
+//
+// Loads cover only a page's rows below kv_len: the tail of a sequence's last
+// page is outside the buffer range and reads as zeros without a memory access.
+//
 // Fused append (optional): when the caller passes the step's new K/V rows,
 // the workgroup that owns a sequence's last page writes the new row to
 // slot_mapping's slot and patches the copy it loaded, so a decode step costs
@@ -62,6 +73,7 @@ constexpr int kWorkInts = 8;
 constexpr int kMaxWaves = 8;      // waves per workgroup (one per KV head), at most
 constexpr int kGroupHeads = 4;    // KV heads per workgroup (its slice of each page row)
 constexpr int kMaxPartPages = 64; // a partition's page ids fit one wave-wide load
+constexpr int kMaxPackSeqs = 16;  // sequences per pack (one lane each; patch bits)
 
 // Layout of one partition's partial output: per (slot, KV head), NGR groups
 // of 4 head rows, each NDB dim blocks of 16 lanes x 4 rows (float4 per
@@ -199,10 +211,11 @@ __device__ __forceinline__ void merge_head(T* __restrict__ out, float* wts, int 
 // pages ahead, copied into a padded LDS tile, and each wave reads its heads'
 // columns from there: K rows as the A operand of the QK MFMA (ds_read_b128),
 // V through ds_read_b64_tr_b16 as the B operand of the PV MFMA.
-template <typename T, int D, int G, int HPW>
+template <typename T, int D, int G, int HPW, bool PACK>
 __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     const T* __restrict__ q, T* __restrict__ out, T* __restrict__ kpool, T* __restrict__ vpool,
     int64_t num_blocks, const int32_t* __restrict__ kv_indices,
+    const int32_t* __restrict__ kv_indptr, const int32_t* __restrict__ kv_lens,
     const int32_t* __restrict__ work, int32_t n_kv_heads, float scale_log2,
     const T* __restrict__ k_new, const T* __restrict__ v_new,
     const int32_t* __restrict__ slot_mapping, float* part_o, float* part_ml,
@@ -234,8 +247,34 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   int* s_flag = reinterpret_cast<int*>(smem + max(kBufs * 2 * PS * RS, NW * 64 * 4 * NGR * 4));
 
   const int32_t* w = work + kWorkInts * wi;
-  const int seq = w[0], pbase = w[1], npp = w[2], slot = w[3];
-  const int kv_len = w[4], tok0 = w[5], nparts = w[6], slot0 = w[7];
+  const int seq0 = w[0], pbase = w[1], npp = w[2], slot = w[3];
+  const int tok0 = w[5], nparts = w[6], slot0 = w[7];
+  // A pack holds w[4] whole consecutive sequences from seq0 (segments), whose
+  // pages follow each other in kv_indices from pbase: lane s < nseq holds
+  // segment s's first page within the pack and its kv_len. Otherwise the
+  // partition is one segment and w[4] its sequence's kv_len.
+  int nseq = 1, lane_first = 0, lane_kv = w[4], lane_slot = 0;
+  if constexpr (PACK) {
+    nseq = w[4];
+    if (lane < nseq) {
+      lane_first = kv_indptr[seq0 + lane] - pbase;
+      lane_kv = kv_lens[seq0 + lane];
+      if (k_new != nullptr) lane_slot = slot_mapping[seq0 + lane];
+    }
+  }
+  auto seg_of = [&](int j) -> int {  // segment of page j (wave-uniform)
+    if constexpr (!PACK) return 0;
+    return __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < nseq && lane_first <= j)) - 1;
+  };
+  auto seg_first = [&](int s) { return PACK ? __builtin_amdgcn_readlane(lane_first, s) : 0; };
+  auto seg_end = [&](int s) {        // one past the segment's last page
+    return PACK && s + 1 < nseq ? __builtin_amdgcn_readlane(lane_first, s + 1) : npp;
+  };
+  auto seg_kv = [&](int s) { return __builtin_amdgcn_readlane(lane_kv, s); };
+  // first token of page j within its sequence
+  auto page_tok = [&](int j, int s) { return PACK ? (j - seg_first(s)) * 16 : tok0 + j * 16; };
+  int seq = seq0;                    // sequence of the segment being computed
+  const int kv_len = seg_kv(0);
   const int Hq = n_kv_heads * G;
   const int64_t row = (int64_t)n_kv_heads * D;
   const int n = lane & 15;   // MFMA row/column within a 16-lane block
@@ -259,11 +298,16 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     goff[k] = (uint32_t)(lrow[k] * frow + hg * rowb + (c - lrow[k] * cpr) * 16);
     loff[k] = (uint32_t)(lrow[k] * RS + (c - lrow[k] * cpr) * 16);
   }
-  const uint32_t page_bytes = (uint32_t)(PS * frow);
+  // Only the page's rows below kv_len are in the buffer range: the rows past
+  // it (the tail of a sequence's last page) read as zeros without a memory
+  // access.
   auto load_page = [&](int j, vec8* kr, vec8* vr) {
     const int64_t page = __builtin_amdgcn_readlane(pid, j);
-    const __amdgpu_buffer_rsrc_t rk = ws_rsrc(kpool + page * PS * row, page_bytes);
-    const __amdgpu_buffer_rsrc_t rv = ws_rsrc(vpool + page * PS * row, page_bytes);
+    const int sj = seg_of(j);
+    const int live = min(PS, seg_kv(sj) - page_tok(j, sj));
+    const uint32_t bytes = (uint32_t)live * (uint32_t)frow;
+    const __amdgpu_buffer_rsrc_t rk = ws_rsrc(kpool + page * PS * row, bytes);
+    const __amdgpu_buffer_rsrc_t rv = ws_rsrc(vpool + page * PS * row, bytes);
 #pragma unroll
     for (int k = 0; k < CPL; ++k) {
       kr[k] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(rk, goff[k], 0, kNt));
@@ -276,32 +320,39 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
 
   // Q^T as the QK B operand per owned head: column n = query head h*G + n.
   vec8 qb[HPW][NCH];
+  auto load_q = [&](auto& dst, int sq) {
 #pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) {
-    const int h = hg * HGW + wave + hh * NW;
-    const T* qr = q + ((int64_t)seq * Hq + h * G + (n < G ? n : 0)) * D + g * 8;
+    for (int hh = 0; hh < HPW; ++hh) {
+      const int h = hg * HGW + wave + hh * NW;
+      const T* qr = q + ((int64_t)sq * Hq + h * G + (n < G ? n : 0)) * D + g * 8;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      vec8 t = *reinterpret_cast<const vec8*>(qr + c * 32);
-      qb[hh][c] = (n < G) ? t : vec8{};
+      for (int c = 0; c < NCH; ++c) {
+        vec8 t = *reinterpret_cast<const vec8*>(qr + c * 32);
+        dst[hh][c] = (n < G) ? t : vec8{};
+      }
     }
+  };
+  load_q(qb, seq0);
+  // a pack's next segment's Q is loaded one segment ahead
+  vec8 qn[PACK ? HPW : 1][PACK ? NCH : 1];
+  if constexpr (PACK) {
+    if (nseq > 1) load_q(qn, seq0 + 1);
   }
 
   // Fused append: the workgroup whose partition holds the newest token writes
   // that row (all heads) to slot_mapping's slot now; the loaded copy of the
   // row is patched before it reaches LDS.
-  const bool owns_last = k_new != nullptr && tok0 + npp * PS >= kv_len;
-  const int tl = (kv_len - 1) % PS;   // newest token's row within its page
-  bool patch = false;
-  if (owns_last) {
-    const int64_t csr_slot = (int64_t)__builtin_amdgcn_readlane(pid, npp - 1) * PS + tl;
-    const int64_t new_slot = slot_mapping[seq];
+  // A pack owns the newest token of every segment. Bit s of `patch` says
+  // whether segment s's loaded copy of its newest row is patched.
+  auto append_row = [&](int sq, int kv, int last_j) -> bool {
+    const int tl = (kv - 1) % PS;   // newest token's row within its page
+    const int64_t csr_slot = (int64_t)__builtin_amdgcn_readlane(pid, last_j) * PS + tl;
+    const int64_t new_slot = slot_mapping[sq];
     const bool in_range = new_slot >= 0 && new_slot < num_blocks * PS;
     if (!in_range && tid == 0) flag(status, PKV_STATUS_BAD_SLOT);
-    patch = new_slot == csr_slot;
     if (in_range) {
-      const unsigned char* kn = reinterpret_cast<const unsigned char*>(k_new + seq * row);
-      const unsigned char* vn = reinterpret_cast<const unsigned char*>(v_new + seq * row);
+      const unsigned char* kn = reinterpret_cast<const unsigned char*>(k_new + sq * row);
+      const unsigned char* vn = reinterpret_cast<const unsigned char*>(v_new + sq * row);
       unsigned char* kd = reinterpret_cast<unsigned char*>(kpool + new_slot * row);
       unsigned char* vd = reinterpret_cast<unsigned char*>(vpool + new_slot * row);
 #pragma unroll
@@ -312,6 +363,26 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
           *reinterpret_cast<vec8*>(vd + col) = *reinterpret_cast<const vec8*>(vn + col);
         }
       }
+    }
+    return new_slot == csr_slot;
+  };
+  uint32_t patch = 0, in_range_bits = 0;
+  if (k_new != nullptr) {
+    if constexpr (PACK) {
+      // every segment ends in the pack: its new row is written, and patched
+      // into the loaded copy, when its last page is staged
+      for (int s = 0; s < nseq; ++s) {
+        const int tl = (seg_kv(s) - 1) % PS;
+        const int64_t csr_slot =
+            (int64_t)__builtin_amdgcn_readlane(pid, seg_end(s) - 1) * PS + tl;
+        const int64_t new_slot = __builtin_amdgcn_readlane(lane_slot, s);
+        const bool in_range = new_slot >= 0 && new_slot < num_blocks * PS;
+        if (!in_range && tid == 0) flag(status, PKV_STATUS_BAD_SLOT);
+        patch |= (uint32_t)(new_slot == csr_slot) << s;
+        in_range_bits |= (uint32_t)in_range << s;
+      }
+    } else if (tok0 + npp * PS >= kv_len) {
+      patch = append_row(seq0, kv_len, npp - 1);
     }
   }
 
@@ -332,9 +403,34 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   auto stage = [&](int j, vec8* kr, vec8* vr) {
     unsigned char* kl = smem + (j & 1) * 2 * PS * RS;
     unsigned char* vl = kl + PS * RS;
-    if (patch && j == npp - 1) {
-      const unsigned char* kn = reinterpret_cast<const unsigned char*>(k_new + seq * row);
-      const unsigned char* vn = reinterpret_cast<const unsigned char*>(v_new + seq * row);
+    const int s = seg_of(j);
+    const int kv = seg_kv(s);
+    if (PACK && ((in_range_bits >> s) & 1) && j == seg_end(s) - 1) {
+      const int sq = seq0 + s, tl = (kv - 1) % PS;
+      const int64_t new_slot = __builtin_amdgcn_readlane(lane_slot, s);
+      const bool pt = (patch >> s) & 1;
+      const unsigned char* kn = reinterpret_cast<const unsigned char*>(k_new + sq * row);
+      const unsigned char* vn = reinterpret_cast<const unsigned char*>(v_new + sq * row);
+      unsigned char* kd = reinterpret_cast<unsigned char*>(kpool + new_slot * row);
+      unsigned char* vd = reinterpret_cast<unsigned char*>(vpool + new_slot * row);
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        if (lrow[k] == tl) {
+          const uint32_t col = goff[k] - (uint32_t)tl * frow;
+          const vec8 kx = *reinterpret_cast<const vec8*>(kn + col);
+          const vec8 vx = *reinterpret_cast<const vec8*>(vn + col);
+          *reinterpret_cast<vec8*>(kd + col) = kx;
+          *reinterpret_cast<vec8*>(vd + col) = vx;
+          if (pt) {
+            kr[k] = kx;
+            vr[k] = vx;
+          }
+        }
+      }
+    } else if (!PACK && ((patch >> s) & 1) && j == seg_end(s) - 1) {
+      const int sq = seq0 + s, tl = (kv - 1) % PS;
+      const unsigned char* kn = reinterpret_cast<const unsigned char*>(k_new + sq * row);
+      const unsigned char* vn = reinterpret_cast<const unsigned char*>(v_new + sq * row);
 #pragma unroll
       for (int k = 0; k < CPL; ++k) {
         if (lrow[k] == tl) {
@@ -344,18 +440,37 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
         }
       }
     }
-    const int tp = tok0 + j * PS;  // first token of the page
+    const int tp = page_tok(j, s);  // first token of the page
 #pragma unroll
     for (int k = 0; k < CPL; ++k) {
       *reinterpret_cast<vec8*>(kl + loff[k]) = kr[k];
       // rows past kv_len are zeroed so stale bits never reach the PV sum
-      *reinterpret_cast<vec8*>(vl + loff[k]) = tp + lrow[k] < kv_len ? vr[k] : vec8{};
+      *reinterpret_cast<vec8*>(vl + loff[k]) = tp + lrow[k] < kv ? vr[k] : vec8{};
+    }
+  };
+  // lane (dim column n, group g) holds heads 4g..4g+3 of dims 16b + n.
+  auto write_out = [&]() {
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      const int h = hg * HGW + wave + hh * NW;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * g + i;
+        const float li = __shfl(l_run[hh], r, 64);  // lane r holds head r's sum
+        if (r < G) {
+#pragma unroll
+          for (int b = 0; b < NDB; ++b)
+            out[((int64_t)seq * Hq + h * G + r) * D + 16 * b + n] = (T)(o[hh][b][i] / li);
+        }
+      }
     }
   };
   auto compute = [&](int j) {
     const unsigned char* kl = smem + (j & 1) * 2 * PS * RS;
     const unsigned char* vl = kl + PS * RS;
-    const int tp = tok0 + j * PS;
+    const int sg = seg_of(j);
+    const int kv = seg_kv(sg);
+    const int tp = page_tok(j, sg);
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
       const int h = wave + hh * NW;  // the head's column in the group's LDS rows
@@ -369,7 +484,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       float mx = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sc[i] = tp + 4 * g + i < kv_len ? acc[i] * scale_log2 : -INFINITY;
+        sc[i] = tp + 4 * g + i < kv ? acc[i] * scale_log2 : -INFINITY;
         mx = fmaxf(mx, sc[i]);
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -409,6 +524,27 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
         o[hh][b] = Mma<T>::pv(p, __builtin_bit_cast(vec4, raw), o[hh][b]);
       }
     }
+    if constexpr (PACK) {
+      // the segment's last page: write its output and start the next
+      // sequence (the last segment leaves through the common exit)
+      if (sg + 1 < nseq && j == seg_end(sg) - 1) {
+        write_out();
+#pragma unroll
+        for (int hh = 0; hh < HPW; ++hh) {
+          m_run[hh] = -INFINITY;
+          l_run[hh] = 0.f;
+#pragma unroll
+          for (int b = 0; b < NDB; ++b) o[hh][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        seq = seq0 + sg + 1;
+#pragma unroll
+        for (int hh = 0; hh < HPW; ++hh) {
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) qb[hh][c] = qn[hh][c];
+        }
+        if (sg + 2 < nseq) load_q(qn, seq + 1);
+      }
+    }
   };
   // Registers: set A holds the even pages, set B the odd ones.
   stage(0, kA, vA);
@@ -427,22 +563,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     }
   }
 
-  // lane (dim column n, group g) holds heads 4g..4g+3 of dims 16b + n.
-  if (slot < 0) {
-#pragma unroll
-    for (int hh = 0; hh < HPW; ++hh) {
-      const int h = hg * HGW + wave + hh * NW;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * g + i;
-        const float li = __shfl(l_run[hh], r, 64);  // lane r holds head r's sum
-        if (r < G) {
-#pragma unroll
-          for (int b = 0; b < NDB; ++b)
-            out[((int64_t)seq * Hq + h * G + r) * D + 16 * b + n] = (T)(o[hh][b][i] / li);
-        }
-      }
-    }
+  if (PACK || slot < 0) {
+    write_out();
     return;
   }
 
@@ -494,22 +616,29 @@ static size_t decode_lds_bytes(int32_t Hkv, int32_t D, int32_t G) {
 
 template <typename T, int D, int G, int HPW>
 static void launch(const void* q, void* out, void* kp, void* vp, int64_t nb,
-                   const int32_t* indices, const int32_t* work, int32_t n_work, int32_t Hkv,
+                   const int32_t* indices, const int32_t* indptr, const int32_t* kv_lens,
+                   bool pack, const int32_t* work, int32_t n_work, int32_t Hkv,
                    float sl2, const void* kn, const void* vn, const int32_t* slots, float* po,
                    float* pml, uint32_t o_bytes, uint32_t ml_bytes, int32_t* cnt,
                    int32_t* status, hipStream_t s) {
   const int hgw = std::min<int>(Hkv, kGroupHeads);  // KV heads per workgroup
   const int nw = hgw / HPW;
-  hipLaunchKernelGGL((decode_kernel<T, D, G, HPW>), dim3((unsigned)(n_work * (Hkv / hgw))),
-                     dim3(nw * 64), decode_lds_bytes(hgw, D, G), s, (const T*)q, (T*)out, (T*)kp, (T*)vp, nb,
-                     indices, work, Hkv, sl2, (const T*)kn, (const T*)vn, slots, po, pml, o_bytes,
-                     ml_bytes, cnt, status);
+  const dim3 grid((unsigned)(n_work * (Hkv / hgw))), block(nw * 64);
+  const size_t lds = decode_lds_bytes(hgw, D, G);
+  if (pack)
+    hipLaunchKernelGGL((decode_kernel<T, D, G, HPW, true>), grid, block, lds, s, (const T*)q,
+                       (T*)out, (T*)kp, (T*)vp, nb, indices, indptr, kv_lens, work, Hkv, sl2,
+                       (const T*)kn, (const T*)vn, slots, po, pml, o_bytes, ml_bytes, cnt, status);
+  else
+    hipLaunchKernelGGL((decode_kernel<T, D, G, HPW, false>), grid, block, lds, s, (const T*)q,
+                       (T*)out, (T*)kp, (T*)vp, nb, indices, indptr, kv_lens, work, Hkv, sl2,
+                       (const T*)kn, (const T*)vn, slots, po, pml, o_bytes, ml_bytes, cnt, status);
 }
 
 typedef void (*LaunchFn)(const void*, void*, void*, void*, int64_t, const int32_t*,
-                         const int32_t*, int32_t, int32_t, float, const void*, const void*,
-                         const int32_t*, float*, float*, uint32_t, uint32_t, int32_t*,
-                         int32_t*, hipStream_t);
+                         const int32_t*, const int32_t*, bool, const int32_t*, int32_t, int32_t,
+                         float, const void*, const void*, const int32_t*, float*, float*,
+                         uint32_t, uint32_t, int32_t*, int32_t*, hipStream_t);
 
 template <typename T, int D, int HPW>
 static LaunchFn pick_g(int G) {
@@ -602,6 +731,26 @@ extern "C" int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_lens,
     }
     if (parts > 1) slots += parts;
   }
+  if (slots == 0) {
+    // No sequence is split: runs of consecutive sequences (their pages are
+    // consecutive in kv_indices) share a partition, up to part_pages pages
+    // and kMaxPackSeqs sequences, so a workgroup's start-up latency is paid
+    // once per pack instead of once per short sequence. Entry: {first seq,
+    // its first page index, pages of the pack, -1, sequences in the pack, 0,
+    // 1, -1}.
+    items.clear();
+    for (int32_t i = 0; i < n_seqs;) {
+      int32_t j = i, pages = 0;
+      while (j < n_seqs && j - i < kMaxPackSeqs) {
+        const int32_t np = kv_indptr[j + 1] - kv_indptr[j];
+        if (j > i && pages + np > part_pages) break;
+        pages += np;
+        ++j;
+      }
+      items.push_back({{i, kv_indptr[i], pages, -1, j - i, 0, 1, -1}});
+      i = j;
+    }
+  }
   // Longest partitions first, so the short tail items fill in behind them;
   // among equals, longer sequences first so their merges start early.
   std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) {
@@ -682,8 +831,11 @@ extern "C" int pkv_attend_decode(const void* q, void* out, void* k_pool, void* v
     o_bytes = (uint32_t)(pf * 4);
     ml_bytes = (uint32_t)(mlf * 4);
   }
-  fn(q, out, k_pool, v_pool, num_blocks, kv_indices, plan, n_work, n_kv_heads, scale * kLog2e,
-     k_new, v_new, slot_mapping, po, pml, o_bytes, ml_bytes, cnt, status_word, s);
+  // A plan without partial slots splits no sequence; its partitions are packs
+  // of whole consecutive sequences (pkv_plan_decode).
+  fn(q, out, k_pool, v_pool, num_blocks, kv_indices, kv_indptr, kv_lens, n_slots == 0, plan,
+     n_work, n_kv_heads, scale * kLog2e, k_new, v_new, slot_mapping, po, pml, o_bytes, ml_bytes,
+     cnt, status_word, s);
   PKV_LAUNCH_CHECK();
   return PKV_OK;
 }

@@ -480,3 +480,56 @@ def test_fused_append_with_slot_mapping_off_the_page_table():
     res = p.step(odd, 2)
     check(res, "off-table slot")
     assert torch.equal(p.gpu.k_pool[0].float().cpu(), p.ref.k_pool[0]), "pool bytes differ"
+
+
+# ------------------------------------- packs of short sequences (no split)
+
+@pytest.mark.parametrize("part_pages", [5, 10, 64])
+def test_packed_short_sequences_vs_oracle(part_pages):
+    """A batch with no split sequence runs packs of consecutive whole
+    sequences per workgroup (the 4096-sequence capacity batch is of this
+    kind): every sequence's decode, fused append included, matches the
+    oracle, across segment boundaries inside a pack."""
+    print(f"packed short sequences part_pages={part_pages}", flush=True)
+    rng = np.random.default_rng(part_pages)
+    lens = [int(x) for x in rng.integers(1, 64, 300)] + [16, 17, 1, 64]
+    p = Pair(1, 1024, 16, 8, 32, 64, part_pages=part_pages)
+    alloc = BlockAllocator(1024, 16)
+    alloc.allocate(1024)
+    alloc.free(torch.randperm(1024, generator=torch.Generator().manual_seed(2)).tolist())
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(len(lens))]
+    check(p.step(grow_and_assemble(seqs, lens, 16), 1), "packed history")
+    for step in range(2):
+        meta = grow_and_assemble(seqs, [1] * len(lens), 16)
+        check(p.step(meta, 10 + step), f"packed decode step {step}")
+        plan = p.gpu._planned
+        assert plan.n_slots == 0 and plan.n_work < len(lens), "expected packed partitions"
+
+
+def test_packed_sequence_equals_solo_bitwise():
+    """A sequence decoded inside a pack gives the same bits as decoded alone,
+    and as inside a batch whose other sequences are split."""
+    print("packed vs solo vs split-batch bitwise", flush=True)
+    g = torch.Generator().manual_seed(9)
+    lens = [5, 40, 100, 17, 63]
+    bk = MI355XBackend(1, 256, 16, 8, 32, 64, device=DEV, part_pages=64)
+    a = BlockAllocator(256, 16)
+    seqs = [SequenceBlocks(a, seq_id=i) for i in range(len(lens) + 1)]
+    hist = make_meta_grow(seqs[:-1], lens, device=DEV)
+    T = sum(lens)
+    bk.append_kv(0, torch.randn(T, 8, 64, generator=g).half().to(DEV),
+                 torch.randn(T, 8, 64, generator=g).half().to(DEV), hist)
+    long_hist = make_meta_grow(seqs[-1:], [1100], device=DEV)   # 69 pages: split
+    bk.append_kv(0, torch.randn(1100, 8, 64, generator=g).half().to(DEV),
+                 torch.randn(1100, 8, 64, generator=g).half().to(DEV), long_hist)
+    q = torch.randn(len(seqs), 32, 64, generator=g).half().to(DEV)
+    for s in seqs:
+        s.append(1)
+    packed = bk.attend(q[:-1], 0, 0.125, make_meta(seqs[:-1], [1] * len(lens), 16, device=DEV))
+    assert bk._planned.n_slots == 0 and bk._planned.n_work == 1, "expected one pack"
+    mixed = bk.attend(q, 0, 0.125, make_meta(seqs, [1] * len(seqs), 16, device=DEV))
+    assert bk._planned.n_slots > 0, "expected the long sequence to be split"
+    for i in range(len(lens)):
+        solo = bk.attend(q[i:i + 1], 0, 0.125, make_meta([seqs[i]], [1], 16, device=DEV))
+        assert torch.equal(solo, packed[i:i + 1]), f"seq {i}: pack changed the bits"
+        assert torch.equal(solo, mixed[i:i + 1]), f"seq {i}: split batch changed the bits"

@@ -79,6 +79,29 @@ def test_decode_plan_covers_every_page_once(part_pages):
     assert list(work[:, 2]) == sorted(work[:, 2], reverse=True), "longest partitions first"
 
 
+@pytest.mark.parametrize("part_pages", [1, 4, 10, 64])
+def test_decode_plan_packs_consecutive_sequences_when_none_is_split(part_pages):
+    """No sequence longer than a partition: the plan has no partial slots and
+    each entry is a maximal run of consecutive whole sequences (at most 16,
+    at most part_pages pages unless a single sequence), longest first."""
+    rng = random.Random(part_pages)
+    kv_lens = [rng.randint(1, 16 * part_pages) for _ in range(500)] + [16 * part_pages, 1]
+    indptr, npages, work, n_slots = plan_decode(kv_lens, part_pages)
+    assert n_slots == 0
+    seen = []
+    for seq0, pbase, pages, slot, nseq, tok0, nparts, slot0 in work:
+        assert (slot, tok0, nparts, slot0) == (-1, 0, 1, -1)
+        assert 1 <= nseq <= 16 and pbase == indptr[seq0]
+        assert pages == indptr[seq0 + nseq] - indptr[seq0]
+        assert pages <= part_pages
+        nxt = seq0 + nseq
+        if nxt < len(kv_lens) and nseq < 16:
+            assert pages + npages[nxt] > part_pages, "pack could have taken the next sequence"
+        seen.extend(range(seq0, nxt))
+    assert sorted(seen) == list(range(len(kv_lens))), "every sequence in exactly one pack"
+    assert list(work[:, 2]) == sorted(work[:, 2], reverse=True), "longest packs first"
+
+
 def test_decode_plan_rejects_partitions_beyond_one_wave():
     lib = _native.load()
     indptr = np.array([0, 1], np.int32)
