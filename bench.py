@@ -277,7 +277,7 @@ def bench_decode(args):
         "host_side_ms": {"batch_meta_build_upload": round(r["meta_ms"], 3),
                          "plan_incl_device_to_host_sync": round(r["plan_ms"], 3)},
         "roofline": {
-            "kernel": "pkv::decode_kernel<_Float16,64,4,1> (KV append fused), one launch per layer",
+            "kernel": "pkv::decode_kernel<_Float16,64,4,1,false> (split-K partitions, KV append fused), one launch per layer",
             "bound": "hbm", "achieved": round(r["kern_gbps"], 1), "peak": PEAK_HBM_GBPS,
             "unit": "GB/s", "frac": round(r["kern_gbps"] / PEAK_HBM_GBPS, 4),
             "traffic": traffic_for("decode_kernel_batch256"),
