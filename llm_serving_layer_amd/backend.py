@@ -66,7 +66,14 @@ def unavailable_reason() -> str | None:
     return _native.reason()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _current_stream(device: torch.device) -> int:
+    """Handle of torch's current stream on ``device`` (the raw-handle query
+    skips building a Stream object on every launch)."""
+    if _raw_stream is not None and device.index is not None:
+        return _raw_stream(device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 
