@@ -81,7 +81,15 @@ class _Plan:
     """Device-side metadata and launch plan for one BatchMeta (one step)."""
 
     __slots__ = ("meta", "use_prefill", "slots", "indptr", "indices", "kv_lens", "cu_q",
-                 "bidx", "plan", "n_work", "n_slots", "n_tokens", "n_seqs", "fusable")
+                 "bidx", "plan", "n_work", "n_slots", "n_tokens", "n_seqs", "fusable", "dec")
+
+
+class _DecodeRows:
+    """The one-token sequences of a mixed batch, run through the decode kernel:
+    their token rows in q/out, and their paging metadata and decode plan as a
+    batch of their own."""
+
+    __slots__ = ("rows", "indptr", "indices", "kv_lens", "plan", "n", "n_work", "n_slots")
 
 
 class _Pending:
@@ -147,6 +155,10 @@ class MI355XBackend:
         self._fast_decode = bool(self._lib.pkv_decode_fast_path(
             n_heads, n_kv_heads, head_dim, block_size, self._code, part_pages))
         self._fuse_append = fuse_append and self._fast_decode
+        # A mixed batch (prefill chunks beside one-token decodes) runs its
+        # decodes through the decode kernel, so a decode step's bits do not
+        # depend on whether prefills share its batch.
+        self._split_mixed = self._fast_decode and self.q_tile == self._prefill_tile > 0
 
         self._pool = torch.zeros((num_layers, 2, num_blocks, block_size, n_kv_heads, head_dim),
                                  dtype=dtype, device=self.device)
@@ -370,17 +382,9 @@ class MI355XBackend:
         vp = self._v_pool[layer_idx].data_ptr()
         self.n_runs += 1
         if not p.use_prefill:
-            ws = self._workspace
-            rc = self._lib.pkv_attend_decode(
-                q.data_ptr(), out.data_ptr(), kp, vp, self.num_blocks, p.indptr.data_ptr(),
-                p.indices.data_ptr(), p.kv_lens.data_ptr(), p.n_seqs, self.n_heads,
-                self.n_kv_heads, self.head_dim, self.block_size, float(scale), self._code,
-                p.plan.data_ptr(), p.n_work, p.n_slots, self.part_pages,
-                pend.k.data_ptr() if fused else None, pend.v.data_ptr() if fused else None,
-                p.slots.data_ptr() if fused else None,
-                ws.data_ptr() if ws.numel() else None, ws.numel(), self._status.data_ptr(),
-                stream)
-            _native.check(rc, "attend (decode)")
+            self._launch_decode(q, out, kp, vp, p.indptr, p.indices, p.kv_lens, p.n_seqs,
+                                p.plan, p.n_work, p.n_slots, scale, stream,
+                                pend if fused else None, p.slots)
         else:
             rc = self._lib.pkv_attend_prefill(
                 q.data_ptr(), out.data_ptr(), kp, vp, self.num_blocks, p.cu_q.data_ptr(),
@@ -389,7 +393,26 @@ class MI355XBackend:
                 self.head_dim, self.block_size, float(scale), self._code, p.plan.data_ptr(),
                 p.n_work, self.q_tile, self._status.data_ptr(), stream)
             _native.check(rc, "attend (prefill)")
+            d = p.dec
+            if d is not None:
+                qd = q.index_select(0, d.rows)
+                od = torch.empty_like(qd)
+                self._launch_decode(qd, od, kp, vp, d.indptr, d.indices, d.kv_lens, d.n,
+                                    d.plan, d.n_work, d.n_slots, scale, stream, None, None)
+                out.index_copy_(0, d.rows, od)
         return out
+
+    def _launch_decode(self, q, out, kp, vp, indptr, indices, kv_lens, n_seqs, plan, n_work,
+                       n_slots, scale, stream, pend, slots) -> None:
+        ws = self._workspace
+        rc = self._lib.pkv_attend_decode(
+            q.data_ptr(), out.data_ptr(), kp, vp, self.num_blocks, indptr.data_ptr(),
+            indices.data_ptr(), kv_lens.data_ptr(), n_seqs, self.n_heads, self.n_kv_heads,
+            self.head_dim, self.block_size, float(scale), self._code, plan.data_ptr(), n_work,
+            n_slots, self.part_pages, pend.k.data_ptr() if pend else None,
+            pend.v.data_ptr() if pend else None, slots.data_ptr() if pend else None,
+            ws.data_ptr() if ws.numel() else None, ws.numel(), self._status.data_ptr(), stream)
+        _native.check(rc, "attend (decode)")
 
     # -- planning ---------------------------------------------------------------
 
@@ -447,37 +470,29 @@ class MI355XBackend:
         i32 = lambda a: np.ascontiguousarray(a, dtype=np.int32)  # noqa: E731
         kvl32, indptr32, last32, cu32 = i32(kvl), i32(indptr), i32(last), i32(cu)
         ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
-        n_work, n_slots = C.c_int32(), C.c_int32()
+        decodes = None
         if not use_prefill:
-            cap = 8 * (int(indptr[-1]) + n)
-            buf = np.empty(cap, dtype=np.int32)
-            rc = self._lib.pkv_plan_decode(ptr(indptr32), ptr(kvl32), ptr(last32), n,
-                                           self.block_size, self.part_pages, ptr(buf), cap,
-                                           C.byref(n_work), C.byref(n_slots))
-            _native.check(rc, "plan (decode)")
-            used = 8 * n_work.value
-            need = self._lib.pkv_decode_workspace_bytes(n, n_slots.value, self.n_heads,
-                                                        self.n_kv_heads, self.head_dim)
-            if need > self._workspace.numel():
-                # zero-filled: the arrival counters at the front start at zero
-                self._workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)
-            elif need > 0:
-                # a previous layout may have left partial data where counters now sit
-                counter_bytes = (4 * n * self.n_kv_heads + 255) // 256 * 256
-                self._workspace[:counter_bytes].zero_()
+            plan, p.n_work, p.n_slots = self._plan_decode(indptr32, kvl32, last32, n)
         else:
+            n_work = C.c_int32()
             cap = 4 * (int(cu[-1]) // self.q_tile + n + 1)
             buf = np.empty(cap, dtype=np.int32)
             rc = self._lib.pkv_plan_prefill(ptr(cu32), ptr(indptr32), ptr(kvl32), ptr(last32),
                                             n, self.block_size, self.q_tile, ptr(buf), cap,
                                             C.byref(n_work))
             _native.check(rc, "plan (prefill)")
-            used = 4 * n_work.value
-        p.n_work, p.n_slots = n_work.value, n_slots.value
-        p.plan = torch.from_numpy(buf[:used].copy()).to(self.device)
+            tiles = buf[:4 * n_work.value].reshape(-1, 4)
+            if self._split_mixed and bool((ql == 1).any()):
+                decodes = np.flatnonzero(ql == 1)
+                tiles = tiles[ql[tiles[:, 0]] > 1]  # the decode kernel takes the rest
+            plan, p.n_work, p.n_slots = tiles.reshape(-1).copy(), tiles.shape[0], 0
+        p.plan = torch.from_numpy(plan).to(self.device)
         p.indptr = self._dev_i32(meta.kv_indptr)
         p.indices = self._dev_i32(meta.kv_indices)
         p.kv_lens = self._dev_i32(meta.kv_lens)
+        p.dec = None
+        if decodes is not None:
+            p.dec = self._decode_rows(decodes, cu, indptr, kvl, last, p.indices)
         p.cu_q = self._dev_i32(meta.cu_query_lens)
         p.bidx = self._dev_i32(meta.batch_indices)
         p.slots = (self._dev_i32(meta.slot_mapping) if meta.slot_mapping is not None
@@ -485,6 +500,47 @@ class MI355XBackend:
         self._planned = p
         self.n_plans += 1
         return p
+
+    def _plan_decode(self, indptr32, kvl32, last32, n):
+        """Host decode plan (pkv_plan_decode) plus a workspace large enough for it."""
+        ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
+        n_work, n_slots = C.c_int32(), C.c_int32()
+        cap = 8 * (int(indptr32[-1]) + n)
+        buf = np.empty(cap, dtype=np.int32)
+        rc = self._lib.pkv_plan_decode(ptr(indptr32), ptr(kvl32), ptr(last32), n,
+                                       self.block_size, self.part_pages, ptr(buf), cap,
+                                       C.byref(n_work), C.byref(n_slots))
+        _native.check(rc, "plan (decode)")
+        need = self._lib.pkv_decode_workspace_bytes(n, n_slots.value, self.n_heads,
+                                                    self.n_kv_heads, self.head_dim)
+        if need > self._workspace.numel():
+            # zero-filled: the arrival counters at the front start at zero
+            self._workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)
+        elif need > 0:
+            # a previous layout may have left partial data where counters now sit
+            counter_bytes = (4 * n * self.n_kv_heads + 255) // 256 * 256
+            self._workspace[:counter_bytes].zero_()
+        return buf[:8 * n_work.value].copy(), n_work.value, n_slots.value
+
+    def _decode_rows(self, dec, cu, indptr, kvl, last, indices_dev) -> _DecodeRows:
+        """The decode-kernel batch of a mixed batch's one-token sequences
+        ``dec``: their own CSR over a gathered copy of their page ids."""
+        npg = indptr[dec + 1] - indptr[dec]
+        sub_ptr = np.concatenate([[0], np.cumsum(npg)])
+        # position in the batch's kv_indices of every page of the sub-batch
+        page_ix = np.repeat(indptr[dec] - sub_ptr[:-1], npg) + np.arange(int(sub_ptr[-1]))
+        i32 = lambda a: np.ascontiguousarray(a, dtype=np.int32)  # noqa: E731
+        d = _DecodeRows()
+        d.n = int(dec.shape[0])
+        plan, d.n_work, d.n_slots = self._plan_decode(i32(sub_ptr), i32(kvl[dec]),
+                                                      i32(last[dec]), d.n)
+        dev = self.device
+        d.plan = torch.from_numpy(plan).to(dev)
+        d.rows = torch.from_numpy(cu[dec].astype(np.int64)).to(dev)
+        d.indptr = torch.from_numpy(i32(sub_ptr)).to(dev)
+        d.kv_lens = torch.from_numpy(i32(kvl[dec])).to(dev)
+        d.indices = indices_dev.index_select(0, torch.from_numpy(page_ix.astype(np.int64)).to(dev))
+        return d
 
     def invalidate_plan(self) -> None:
         """Force the next ``attend`` to re-plan (and drop the cached meta)."""

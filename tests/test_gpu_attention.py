@@ -533,3 +533,29 @@ def test_packed_sequence_equals_solo_bitwise():
         solo = bk.attend(q[i:i + 1], 0, 0.125, make_meta([seqs[i]], [1], 16, device=DEV))
         assert torch.equal(solo, packed[i:i + 1]), f"seq {i}: pack changed the bits"
         assert torch.equal(solo, mixed[i:i + 1]), f"seq {i}: split batch changed the bits"
+
+
+def test_mixed_batch_decodes_equal_pure_decode_bitwise():
+    """Prefill chunks and one-token decodes in one batch: each decode token's
+    output has the same bits as the same decode run alone (the decodes of a
+    mixed batch take the decode kernel), and the whole batch matches the
+    oracle."""
+    print("mixed prefill + decode batch", flush=True)
+    p = Pair(1, 256, 16, 8, 32, 64, part_pages=4)
+    a = BlockAllocator(256, 16)
+    seqs = [SequenceBlocks(a, seq_id=i) for i in range(5)]
+    check(p.step(grow_and_assemble(seqs, [40, 300, 7, 90, 500], 16), 1), "mixed history")
+    meta = grow_and_assemble(seqs, [1, 24, 1, 70, 1], 16)
+    res = p.step(meta, 2)
+    check(res, "mixed step")
+    assert p.gpu._planned.dec is not None and p.gpu._planned.dec.n == 3
+    mixed = res[0][1]
+    cu = meta.cu_query_lens.tolist()
+    g = torch.Generator().manual_seed(2)   # the q the step drew (after k, v)
+    T = meta.n_tokens
+    p.rand((T, 8, 64), g), p.rand((T, 8, 64), g)
+    q = p.rand((T, 32, 64), g).to(DEV)
+    for i in (0, 2, 4):
+        solo = p.gpu.attend(q[cu[i]:cu[i] + 1], 0, 0.125,
+                            make_meta([seqs[i]], [1], 16, device=DEV))
+        assert torch.equal(solo, mixed[cu[i]:cu[i] + 1]), f"decode {i} changed beside prefills"

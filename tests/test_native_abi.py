@@ -191,7 +191,8 @@ def _host_backend(part_pages=10):
     bk.num_layers, bk.num_blocks, bk.block_size = 1, 64, 16
     bk.n_kv_heads, bk.n_heads, bk.head_dim = 8, 32, 64
     bk.part_pages = part_pages
-    bk.q_tile = bk._lib.pkv_prefill_q_tile(32, 8, 64, 16, _native.DTYPE_F16)
+    bk.q_tile = bk._prefill_tile = bk._lib.pkv_prefill_q_tile(32, 8, 64, 16, _native.DTYPE_F16)
+    bk._split_mixed = True
     bk._workspace = torch.zeros(0, dtype=torch.uint8)
     bk._planned, bk._slot_cache, bk._pending = None, None, None
     bk.n_plans = bk.n_runs = 0
@@ -216,3 +217,30 @@ def test_backend_plans_decode_and_prefill_through_the_library():
     assert p.plan.numel() == 8 * p.n_work
     assert bk._workspace.numel() >= bk._lib.pkv_decode_workspace_bytes(
         3, p.n_slots, 32, 8, 64)
+
+
+def test_mixed_batch_plans_its_decodes_for_the_decode_kernel():
+    """Prefill chunks beside one-token decodes: the prefill tiles cover only
+    the multi-token sequences, and the one-token sequences form a decode
+    batch of their own (rows, CSR over their own pages, plan)."""
+    from llm_serving_layer_amd import BlockAllocator, SequenceBlocks
+
+    from ._util import grow_and_assemble
+
+    bk = _host_backend(part_pages=2)
+    alloc = BlockAllocator(64, 16)
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(4)]
+    grow_and_assemble(seqs, [40, 100, 7, 20], 16)
+    meta = grow_and_assemble(seqs, [1, 30, 1, 5], 16)
+    p = bk._ensure_planned(meta)
+    assert p.use_prefill and p.dec is not None
+    tiles = p.plan.reshape(-1, 4).numpy()
+    assert set(tiles[:, 0]) == {1, 3}, "prefill tiles must skip the one-token sequences"
+    d = p.dec
+    assert d.n == 2 and d.rows.tolist() == [0, 31]   # token rows of sequences 0 and 2
+    assert d.kv_lens.tolist() == [41, 8]
+    indptr, indices = meta.kv_indptr.tolist(), meta.kv_indices.tolist()
+    want = indices[indptr[0]:indptr[1]] + indices[indptr[2]:indptr[3]]
+    assert d.indices.tolist() == want and d.indptr.tolist() == [0, 3, 4]
+    work = d.plan.reshape(-1, 8).numpy()
+    assert d.n_slots > 0 and set(work[:, 0]) == {0, 1}, "decode plan over the sub-batch"
