@@ -17,12 +17,13 @@ allocator hand the blocks to another sequence mid-copy
 (preemption.py:355-360). Here one gather kernel packs the victim's blocks
 into a device staging buffer on a side stream, the caller's stream is made to
 wait for THAT (a ~0.1 ms HBM-bound kernel), and only the slow PCIe transfer
-from staging to pinned host memory overlaps with later compute. So freeing
-right after ``swap_out`` returns is safe: any kernel that could overwrite
-those blocks is ordered after the gather. Swap-in mirrors it: H2D into
-staging on the side stream, then a scatter kernel that waits for the caller's
-stream (earlier users of the new blocks), and the caller's stream waits for
-the scatter.
+from staging to pinned host memory, on a transfer stream of its own, overlaps
+with later compute and with the next victim's gather. So freeing right after
+``swap_out`` returns is safe: any kernel that could overwrite those blocks is
+ordered after the gather. Swap-in mirrors it: H2D into staging on the
+transfer stream, then a scatter kernel on the side stream that also waits for
+the caller's stream (earlier users of the new blocks), and the caller's
+stream waits for the scatter.
 """
 
 from __future__ import annotations
@@ -104,7 +105,10 @@ class KVSwapSpace:
         self.device = backend.device
         self.dtype = backend.dtype
         self.pinned = True
+        # kernels (gather / scatter) on one side stream, host transfers on
+        # another, so one sequence's transfer overlaps the next one's kernel
         self._side = torch.cuda.Stream(device=self.device)
+        self._copy = torch.cuda.Stream(device=self.device)
 
     def bytes_for(self, num_blocks: int) -> int:
         return 2 * self.backend.num_layers * num_blocks * self.backend._block_bytes
@@ -117,7 +121,11 @@ class KVSwapSpace:
         for b in block_ids:
             if not 0 <= b < self.backend.num_blocks:
                 raise IndexError(f"block id {b} outside [0, {self.backend.num_blocks})")
-        return torch.tensor(list(block_ids), dtype=torch.int32).to(self.device)
+        # from pinned memory, so the upload is queued on the caller's stream
+        # instead of waiting for it (the side stream waits for that stream
+        # before its kernel reads the ids)
+        host = torch.tensor(list(block_ids), dtype=torch.int32).pin_memory()
+        return host.to(self.device, non_blocking=True)
 
     def _shape(self, nb: int) -> tuple:
         b = self.backend
@@ -153,11 +161,17 @@ class KVSwapSpace:
                                               side.cuda_stream)
                 _native.check(rc, "swap_out gather")
                 ids.record_stream(side)
-                # The blocks may be reused by the caller's stream once packed.
-                main.wait_stream(side)
+                packed = torch.cuda.Event()
+                packed.record(side)
+            # The blocks may be reused by the caller's stream once packed.
+            main.wait_stream(side)
+            copy = self._copy
+            copy.wait_event(packed)
+            with torch.cuda.stream(copy):
                 host.copy_(staging, non_blocking=True)
+                staging.record_stream(copy)
                 done = torch.cuda.Event()
-                done.record(side)
+                done.record(copy)
         self.last_swap_out_seconds = time.perf_counter() - t0
         h = SwapHandle(request_id, blocks.seq_id, blocks.num_tokens, nb, host, want,
                        b.block_size, b.n_kv_heads, b.head_dim, done, staging)
@@ -191,18 +205,24 @@ class KVSwapSpace:
         main = torch.cuda.current_stream(self.device)
         ids = self._ids(blocks.block_ids)
         side = self._side
+        copy = self._copy
         if handle._done is not None:
-            side.wait_event(handle._done)
-        with torch.cuda.stream(side):
+            copy.wait_event(handle._done)
+        with torch.cuda.stream(copy):
             staging = torch.empty(self._shape(nb), dtype=self.dtype, device=self.device)
             staging.copy_(handle._host, non_blocking=True)
-            side.wait_stream(main)  # earlier kernels may still read the new blocks
+            landed = torch.cuda.Event()
+            landed.record(copy)
+        side.wait_event(landed)
+        side.wait_stream(main)  # earlier kernels may still read the new blocks
+        with torch.cuda.stream(side):
             rc = b._lib.pkv_scatter_blocks(b._pool.data_ptr(), b.num_layers, b._plane_bytes,
                                            b._block_bytes, b.num_blocks, ids.data_ptr(), nb,
                                            staging.data_ptr(), b._status.data_ptr(),
                                            side.cuda_stream)
             _native.check(rc, "swap_in scatter")
             ids.record_stream(side)
+            staging.record_stream(side)
         main.wait_stream(side)
 
     def release(self, handle: SwapHandle) -> None:
@@ -218,3 +238,4 @@ class KVSwapSpace:
     def synchronize(self) -> None:
         """Wait for every outstanding swap copy."""
         self._side.synchronize()
+        self._copy.synchronize()
