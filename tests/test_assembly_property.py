@@ -1,0 +1,106 @@
+"""
+Property tests of the host-side path (no GPU): the array-based
+build_batch_meta agrees field by field with an independent per-sequence
+construction (tests/_util.make_meta, the reference's own test-side assembly,
+tests/test_paged_torch.py:66-103) on random ragged batches over fragmented
+pools, and the decode planner covers every page exactly once, split or
+packed, for any lengths and partition size.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+
+import numpy as np
+import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
+
+from llm_serving_layer_amd import (BlockAllocator, ScheduledSeq, SequenceBlocks, _native,
+                                   build_batch_meta)
+
+from ._util import make_meta
+
+SETTINGS = settings(max_examples=60, deadline=None,
+                    suppress_health_check=[HealthCheck.too_slow])
+
+
+@st.composite
+def batches(draw):
+    block_size = draw(st.sampled_from([1, 4, 16, 32]))
+    n = draw(st.integers(1, 24))
+    hist = draw(st.lists(st.integers(0, 300), min_size=n, max_size=n))
+    new = draw(st.lists(st.integers(1, 40), min_size=n, max_size=n))
+    decode_only = draw(st.booleans())
+    if decode_only:
+        new = [1] * n
+    seed = draw(st.integers(0, 2**16))
+    return block_size, hist, new, seed
+
+
+@SETTINGS
+@given(batches())
+def test_array_assembly_equals_per_sequence_assembly(batch):
+    block_size, hist, new, seed = batch
+    need = sum(-(-(h + q) // block_size) for h, q in zip(hist, new))
+    nb = need + 8
+    alloc = BlockAllocator(nb, block_size)
+    rng = np.random.default_rng(seed)
+    alloc.allocate(nb)
+    alloc.free([int(b) for b in rng.permutation(nb)])   # scattered free list
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(len(hist))]
+    for s, h in zip(seqs, hist):
+        if h:
+            s.append(h)
+    for s, q in zip(seqs, new):
+        s.append(q)
+    got = build_batch_meta([ScheduledSeq(s, [0] * q) for s, q in zip(seqs, new)],
+                           device="cpu", page_size=block_size)
+    want = make_meta(seqs, new, block_size)
+    for f in dataclasses.fields(want):
+        a, b = getattr(got, f.name), getattr(want, f.name)
+        if isinstance(b, torch.Tensor):
+            assert a.dtype == b.dtype and torch.equal(a, b), f.name
+        else:
+            assert a == b, f.name
+
+
+@SETTINGS
+@given(st.lists(st.integers(1, 3000), min_size=1, max_size=200), st.integers(1, 64))
+def test_decode_plan_covers_every_page_exactly_once(kv_lens, part_pages):
+    ps = 16
+    n = len(kv_lens)
+    npages = [-(-k // ps) for k in kv_lens]
+    indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
+    kvl = np.array(kv_lens, np.int32)
+    last = np.array([k % ps or ps for k in kv_lens], np.int32)
+    cap = 8 * (int(indptr[-1]) + n)
+    buf = np.empty(cap, np.int32)
+    nw, ns = C.c_int32(), C.c_int32()
+    p = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
+    rc = _native.load().pkv_plan_decode(p(indptr), p(kvl), p(last), n, ps, part_pages,
+                                        p(buf), cap, C.byref(nw), C.byref(ns))
+    _native.check(rc, "plan")
+    work = buf[:8 * nw.value].reshape(-1, 8)
+    covered = np.zeros(int(indptr[-1]), np.int32)
+    if ns.value == 0:   # packs of whole consecutive sequences
+        assert max(npages) <= part_pages
+        for seq0, pbase, pages, slot, nseq, tok0, nparts, slot0 in work:
+            assert pbase == indptr[seq0] and pages == indptr[seq0 + nseq] - pbase
+            assert 1 <= nseq <= 16 and pages <= part_pages
+            covered[pbase:pbase + pages] += 1
+    else:
+        assert max(npages) > part_pages
+        slots = []
+        for seq, pbase, pages, slot, kv, tok0, nparts, slot0 in work:
+            first = pbase - indptr[seq]
+            assert 1 <= pages <= part_pages and kv == kv_lens[seq] and tok0 == first * ps
+            covered[pbase:pbase + pages] += 1
+            if nparts > 1:
+                slots.append(slot)
+            else:
+                assert slot == -1
+        assert sorted(slots) == list(range(ns.value))
+    assert (covered == 1).all()
+    assert list(work[:, 2]) == sorted(work[:, 2], reverse=True)
