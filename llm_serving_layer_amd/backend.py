@@ -272,7 +272,9 @@ class MI355XBackend:
         if len(set(ds)) != len(ds) or set(ds) & {s for s, _ in pairs}:
             raise ValueError("copy_blocks needs distinct destinations that are not also sources")
         self._flush()
-        ids = torch.tensor([s for s, _ in pairs] + ds, dtype=torch.int32).to(self.device)
+        # pinned, so the upload queues on the stream without a host wait
+        ids = torch.tensor([s for s, _ in pairs] + ds, dtype=torch.int32).pin_memory()
+        ids = ids.to(self.device, non_blocking=True)
         n = len(pairs)
         rc = self._lib.pkv_copy_blocks(self._pool.data_ptr(), self.num_layers,
                                        self._plane_bytes, self._block_bytes, self.num_blocks,
@@ -486,7 +488,7 @@ class MI355XBackend:
                 decodes = np.flatnonzero(ql == 1)
                 tiles = tiles[ql[tiles[:, 0]] > 1]  # the decode kernel takes the rest
             plan, p.n_work, p.n_slots = tiles.reshape(-1).copy(), tiles.shape[0], 0
-        p.plan = torch.from_numpy(plan).to(self.device)
+        p.plan = self._upload(plan)
         p.indptr = self._dev_i32(meta.kv_indptr)
         p.indices = self._dev_i32(meta.kv_indices)
         p.kv_lens = self._dev_i32(meta.kv_lens)
@@ -534,13 +536,17 @@ class MI355XBackend:
         d.n = int(dec.shape[0])
         plan, d.n_work, d.n_slots = self._plan_decode(i32(sub_ptr), i32(kvl[dec]),
                                                       i32(last[dec]), d.n)
-        dev = self.device
-        d.plan = torch.from_numpy(plan).to(dev)
-        d.rows = torch.from_numpy(cu[dec].astype(np.int64)).to(dev)
-        d.indptr = torch.from_numpy(i32(sub_ptr)).to(dev)
-        d.kv_lens = torch.from_numpy(i32(kvl[dec])).to(dev)
-        d.indices = indices_dev.index_select(0, torch.from_numpy(page_ix.astype(np.int64)).to(dev))
+        d.plan = self._upload(plan)
+        d.rows = self._upload(cu[dec].astype(np.int64))
+        d.indptr = self._upload(i32(sub_ptr))
+        d.kv_lens = self._upload(i32(kvl[dec]))
+        d.indices = indices_dev.index_select(0, self._upload(page_ix.astype(np.int64)))
         return d
+
+    def _upload(self, a: np.ndarray) -> torch.Tensor:
+        """Host array to the device through pinned memory, queued on the
+        current stream without a host wait."""
+        return torch.from_numpy(a).pin_memory().to(self.device, non_blocking=True)
 
     def invalidate_plan(self) -> None:
         """Force the next ``attend`` to re-plan (and drop the cached meta)."""

@@ -193,6 +193,7 @@ def _host_backend(part_pages=10):
     bk.part_pages = part_pages
     bk.q_tile = bk._prefill_tile = bk._lib.pkv_prefill_q_tile(32, 8, 64, 16, _native.DTYPE_F16)
     bk._split_mixed = True
+    bk._upload = lambda a: torch.from_numpy(np.array(a))   # CPU tensors stand in
     bk._workspace = torch.zeros(0, dtype=torch.uint8)
     bk._planned, bk._slot_cache, bk._pending = None, None, None
     bk.n_plans = bk.n_runs = 0
