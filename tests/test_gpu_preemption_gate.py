@@ -1,10 +1,16 @@
 """
 Greedy tokens under forced preemption are bit-identical to an unpreempted
-run (the reference's phase-3 gate, tests/test_preemption_gpu.py:209-231,
-swap policy), driven through this backend's whole path: chunked prefill of
-the prompts, decode steps with the fused KV append, swap-out of running
-sequences to pinned host memory, their blocks freed and reused by others,
-swap-in into different block ids, and decoding resumed.
+run (the reference's phase-3 gate, tests/test_preemption_gpu.py:209-231),
+driven through this backend's whole path: chunked prefill of the prompts,
+decode steps with the fused KV append, then two running sequences preempted
+and their blocks freed, reused and overwritten by another owner, and resumed:
+- swap policy: their KV goes to pinned host memory and is swapped back into
+  different block ids;
+- recompute policy: their KV is dropped and rebuilt by prefilling the whole
+  history again. Prefill and decode then produce the same KV only if the
+  two paths round alike, so, as the reference suggests for this gate
+  (fp16 prefill and decode kernels round differently), it runs with fp32
+  pools, where both go through the same generic kernel.
 
 The reference's gate needs Llama weights; here a small random model stands
 in. Everything except attention runs per token row in float64 on the host,
@@ -57,7 +63,7 @@ class ToyModel:
         dev = backend.device
         for layer in range(LAYERS):
             def half(a, heads):
-                return torch.from_numpy(a.reshape(len(ids), heads, D)).to(dev, torch.float16)
+                return torch.from_numpy(a.reshape(len(ids), heads, D)).to(dev, backend.dtype)
             q = half(self.rows(h, self.wq[layer]), HQ)
             k = half(self.rows(h, self.wk[layer]), HKV)
             v = half(self.rows(h, self.wv[layer]), HKV)
@@ -69,7 +75,7 @@ class ToyModel:
         return [int(np.argmax(h[i] @ self.head)) for i in last]
 
 
-def generate(model, preempt: bool):
+def generate(model, preempt: bool, policy: str = "swap", dtype=torch.float16):
     """Run every prompt to NEW_TOKENS tokens. With ``preempt`` the victims are
     swapped out at decode step SWAP_AT and their blocks freed; those blocks
     are then taken by other owners and overwritten, and the victims are
@@ -78,7 +84,7 @@ def generate(model, preempt: bool):
     from llm_serving_layer_amd.swap import KVSwapSpace
 
     nb, reserve = 96, 8
-    backend = MI355XBackend(LAYERS, nb, BS, HKV, HQ, D, device="cuda:0", dtype=torch.float16)
+    backend = MI355XBackend(LAYERS, nb, BS, HKV, HQ, D, device="cuda:0", dtype=dtype)
     alloc = BlockAllocator(nb, BS)
     seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(len(PROMPTS))]
     out = [[] for _ in PROMPTS]
@@ -95,7 +101,8 @@ def generate(model, preempt: bool):
         if preempt and step == SWAP_AT:
             for i in VICTIMS:
                 moved[i] = list(seqs[i].block_ids)
-                handles[i] = swap.swap_out(f"req{i}", seqs[i])
+                if policy == "swap":
+                    handles[i] = swap.swap_out(f"req{i}", seqs[i])
                 seqs[i].free()
                 seqs[i] = None
             old = sorted({b for v in moved.values() for b in v})
@@ -110,18 +117,30 @@ def generate(model, preempt: bool):
             for layer in range(LAYERS):
                 for pool in (backend.k_pool[layer], backend.v_pool[layer]):
                     pool.index_copy_(0, ids, torch.randn(pool[ids].shape, generator=g,
-                                                         device=backend.device).half())
+                                                         device=backend.device).to(dtype))
+        just_resumed = set()
         if preempt and step == RESUME_AT:
             alloc.free(fill)
+            redo = []
             for i in VICTIMS:
-                h = handles.pop(i)
                 s = SequenceBlocks(alloc, seq_id=100 + i)
-                s.append(h.num_tokens)
-                swap.swap_in(h, s)
-                swap.release(h)
+                if policy == "swap":
+                    h = handles.pop(i)
+                    s.append(h.num_tokens)
+                    swap.swap_in(h, s)
+                    swap.release(h)
+                else:   # rebuild the KV of the prompt and every generated token
+                    hist = PROMPTS[i] + out[i]
+                    s.append(len(hist))
+                    redo.append((i, ScheduledSeq(s, list(hist))))
                 seqs[i] = s
                 resumed[i] = list(s.block_ids)
-        live = [i for i, o in enumerate(out) if len(o) < NEW_TOKENS and seqs[i] is not None]
+            if redo:
+                for (i, _), t in zip(redo, model.forward(backend, [r for _, r in redo])):
+                    out[i].append(t)
+                    just_resumed.add(i)
+        live = [i for i, o in enumerate(out)
+                if len(o) < NEW_TOKENS and seqs[i] is not None and i not in just_resumed]
         sched = []
         for i in live:
             seqs[i].append(1)
@@ -132,10 +151,13 @@ def generate(model, preempt: bool):
     return out, {"moved": moved, "resumed": resumed, "steps": step}
 
 
-def test_greedy_tokens_are_bit_identical_under_swap_preemption():
+@pytest.mark.parametrize("policy,dtype", [("swap", torch.float16), ("swap", torch.float32),
+                                          ("recompute", torch.float32)])
+def test_greedy_tokens_are_bit_identical_under_preemption(policy, dtype):
+    print(f"preemption gate policy={policy} dtype={dtype}", flush=True)
     model = ToyModel()
-    ref, _ = generate(model, preempt=False)
-    got, info = generate(model, preempt=True)
+    ref, _ = generate(model, preempt=False, dtype=dtype)
+    got, info = generate(model, preempt=True, policy=policy, dtype=dtype)
     # the rig really preempted: both victims were out for several steps and
     # came back into a different block list
     assert set(info["moved"]) == set(VICTIMS) and info["steps"] > RESUME_AT
