@@ -100,25 +100,29 @@ def shuffled_allocator(nb, seed=SEED):
 
 
 def time_eager(step, steps, warmup, per_launch):
-    """K steps through the public API between synchronizations; per-launch
-    HIP events on the current stream (the backend launches there)."""
+    """K steps through the public API between synchronizations, timed with
+    events around the whole run only; then K more steps with HIP events
+    around every launch (on the current stream, where the backend launches)
+    for the per-launch average, which the extra events slow down."""
     import torch
     for _ in range(warmup):
         step(None)
     torch.cuda.synchronize()
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(per_launch)] for _ in range(steps)]
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record()
-    for s in range(steps):
-        step(ev[s])
+    for _ in range(steps):
+        step(None)
     stop.record()
     enqueue = time.perf_counter() - t0
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = start.elapsed_time(stop)
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(per_launch)] for _ in range(steps)]
+    for s in range(steps):
+        step(ev[s])
+    torch.cuda.synchronize()
     launch = [a.elapsed_time(b) for row in ev for a, b in row]
     return {"ms_per_step": max(gpu_ms, wall * 1e3) / steps,
             "gpu_ms_per_step": gpu_ms / steps, "wall_ms_per_step": wall * 1e3 / steps,
