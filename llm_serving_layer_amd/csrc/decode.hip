@@ -255,7 +255,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   // partition is one segment and w[4] its sequence's kv_len.
   int nseq = 1, lane_first = 0, lane_kv = w[4], lane_slot = 0;
   if constexpr (PACK) {
-    nseq = w[4];
+    nseq = min(max(w[4], 1), kMaxPackSeqs);  // the planner's bound; shifts stay in range
     if (lane < nseq) {
       lane_first = kv_indptr[seq0 + lane] - pbase;
       lane_kv = kv_lens[seq0 + lane];
