@@ -559,3 +559,21 @@ def test_mixed_batch_decodes_equal_pure_decode_bitwise():
         solo = p.gpu.attend(q[cu[i]:cu[i] + 1], 0, 0.125,
                             make_meta([seqs[i]], [1], 16, device=DEV))
         assert torch.equal(solo, mixed[cu[i]:cu[i] + 1]), f"decode {i} changed beside prefills"
+
+
+@pytest.mark.parametrize("geom", [(8, 32, 128), (2, 32, 64), (8, 8, 64)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_packed_decode_other_geometries(geom, dtype):
+    """Packs at head_dim 128, 16 query heads per KV head and MHA, fp16 and
+    bf16: a decode batch of short sequences (no split) against the oracle."""
+    n_kv, n_heads, d = geom
+    print(f"packed decode geom={geom} dtype={dtype}", flush=True)
+    tol, rtol = (2e-3, 1e-2) if dtype == torch.float16 else (1.6e-2, 8e-2)
+    p = Pair(1, 512, 16, n_kv, n_heads, d, dtype=dtype, part_pages=8)
+    alloc = BlockAllocator(512, 16)
+    rng = np.random.default_rng(d + n_heads)
+    lens = [int(x) for x in rng.integers(1, 110, 60)]
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(len(lens))]
+    check(p.step(grow_and_assemble(seqs, lens, 16), 1), "history", tol, rtol)
+    check(p.step(grow_and_assemble(seqs, [1] * len(lens), 16), 2), "packed step", tol, rtol)
+    assert p.gpu._planned.n_slots == 0 and p.gpu._planned.n_work < len(lens)
