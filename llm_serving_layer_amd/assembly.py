@@ -8,10 +8,12 @@ are absolute (``kv_len - q .. kv_len - 1``), the CSR triple comes from
 (``has been freed``, ``contributes 0 tokens``, ``blocks.append``,
 ``page_size``).
 
-Different from the reference in one respect that matters on MI355X: all ten
+Different from the reference in two respects that matter on MI355X: all ten
 index arrays are packed into ONE pinned host buffer and uploaded with ONE
-non-blocking copy, then exposed as views. Ten separate ``torch.tensor(...,
-device=...)`` calls are ten synchronous H2D round trips per step.
+non-blocking copy, then exposed as views (ten separate ``torch.tensor(...,
+device=...)`` calls are ten synchronous H2D round trips per step); and the
+host arrays stay attached to the meta (``BatchMeta.host``), so a backend
+plans the step from them instead of copying the device tensors back.
 """
 
 from __future__ import annotations
@@ -22,7 +24,7 @@ from itertools import chain
 import numpy as np
 import torch
 
-from .contract import BatchMeta, validate_host
+from .contract import MIRRORED, BatchMeta, HostMirror, validate_host
 from .paging import SequenceBlocks
 
 __all__ = ["ScheduledSeq", "build_batch_meta", "build_token_tensor"]
@@ -128,7 +130,11 @@ def build_batch_meta(seqs: list[ScheduledSeq], device, page_size: int,
         validate_host(n, page_size, qlens, cu, kvlens, indptr, last, cu[1:] - 1, positions,
                       batch_idx, n_slots=T, n_pages=int(indices.shape[0]))
     fields = _upload(parts, positions, device, dtype_index)
-    return BatchMeta(**fields, page_size=page_size, is_prefill=bool((qlens > 1).any()))
+    # the host arrays travel with the meta, so planning needs no read-back
+    mirror = HostMirror(arrays={k: parts[k] for k in MIRRORED},
+                        of=tuple(fields[k] for k in MIRRORED))
+    return BatchMeta(**fields, page_size=page_size, is_prefill=bool((qlens > 1).any()),
+                     host=mirror)
 
 
 def _upload(parts: dict, positions: np.ndarray, device, dtype_index: torch.dtype) -> dict:

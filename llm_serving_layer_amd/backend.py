@@ -429,20 +429,32 @@ class MI355XBackend:
         if pl is not None and pl.meta is meta:
             return pl
         n = meta.n_seqs
-        parts = [meta.query_lens, meta.cu_query_lens, meta.kv_lens, meta.kv_indptr,
-                 meta.kv_last_page_len]
-        # For the fused append: each sequence's last page id and its new slot.
         with_slots = (meta.slot_mapping is not None and meta.slot_mapping.shape[0] == n
                       and meta.kv_indices.shape[0] > 0 and meta.kv_indptr.shape[0] == n + 1)
-        if with_slots:
-            last_ix = (meta.kv_indptr[1:].to(torch.int64) - 1).clamp(
-                0, meta.kv_indices.shape[0] - 1)
-            parts += [meta.kv_indices[last_ix], meta.slot_mapping]
-        # ONE device->host transfer for everything the host plan reads.
-        host = torch.cat([t.reshape(-1).to(torch.int64) for t in parts]).cpu().numpy()
-        ql, cu = host[:n], host[n:2 * n + 1]
-        kvl, indptr = host[2 * n + 1:3 * n + 1], host[3 * n + 1:4 * n + 2]
-        last = host[4 * n + 2:5 * n + 2]
+        mirror = meta.host_arrays()
+        if mirror is not None:
+            # the assembler's own host arrays: no device read-back
+            ql, cu = mirror["query_lens"], mirror["cu_query_lens"]
+            kvl, indptr = mirror["kv_lens"], mirror["kv_indptr"]
+            last = mirror["kv_last_page_len"]
+            if with_slots:
+                ix = np.clip(indptr[1:] - 1, 0, mirror["kv_indices"].shape[0] - 1)
+                last_page, new_slot = mirror["kv_indices"][ix], mirror["slot_mapping"]
+        else:
+            parts = [meta.query_lens, meta.cu_query_lens, meta.kv_lens, meta.kv_indptr,
+                     meta.kv_last_page_len]
+            # For the fused append: each sequence's last page id and its new slot.
+            if with_slots:
+                last_ix = (meta.kv_indptr[1:].to(torch.int64) - 1).clamp(
+                    0, meta.kv_indices.shape[0] - 1)
+                parts += [meta.kv_indices[last_ix], meta.slot_mapping]
+            # ONE device->host transfer for everything the host plan reads.
+            host = torch.cat([t.reshape(-1).to(torch.int64) for t in parts]).cpu().numpy()
+            ql, cu = host[:n], host[n:2 * n + 1]
+            kvl, indptr = host[2 * n + 1:3 * n + 1], host[3 * n + 1:4 * n + 2]
+            last = host[4 * n + 2:5 * n + 2]
+            if with_slots:
+                last_page, new_slot = host[5 * n + 2:6 * n + 2], host[6 * n + 2:7 * n + 2]
         use_prefill = bool((ql > 1).any())
         if bool(meta.is_prefill) != use_prefill:
             raise ValueError(
@@ -457,7 +469,6 @@ class MI355XBackend:
         # sequence of the launch reads that slot).
         p.fusable = False
         if with_slots and not use_prefill:
-            last_page, new_slot = host[5 * n + 2:6 * n + 2], host[6 * n + 2:7 * n + 2]
             p.fusable = bool((new_slot == last_page * self.block_size + last - 1).all())
         p.n_seqs, p.n_tokens = n, int(cu[-1])
         if p.n_tokens != meta.n_tokens:

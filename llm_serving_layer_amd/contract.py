@@ -20,13 +20,32 @@ that to cache a launch plan by object identity.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Optional, Protocol, runtime_checkable
 
 import numpy as np
 import torch
 
-__all__ = ["BatchMeta", "AttentionBackend", "validate_host"]
+__all__ = ["BatchMeta", "HostMirror", "AttentionBackend", "validate_host"]
+
+#: The index fields a host mirror may carry, in this order.
+MIRRORED = ("query_lens", "cu_query_lens", "kv_lens", "kv_indptr", "kv_indices",
+            "kv_last_page_len", "slot_mapping")
+
+
+@dataclass(frozen=True, eq=False)
+class HostMirror:
+    """
+    Host (int64 numpy) copies of a BatchMeta's index fields, kept by the
+    assembler that built them, so a backend can plan a step without reading
+    the device tensors back. ``of`` holds the device tensors the arrays
+    describe; the mirror speaks for a BatchMeta only while its fields are
+    those very tensors (``BatchMeta.host_arrays``), so a meta rebuilt with
+    ``dataclasses.replace`` never plans from stale arrays.
+    """
+
+    arrays: dict
+    of: tuple
 
 
 @dataclass(frozen=True)
@@ -63,6 +82,18 @@ class BatchMeta:
     last_token_ix: torch.Tensor
     page_size: int = 16
     is_prefill: bool = False
+    host: Optional[HostMirror] = field(default=None, compare=False, repr=False)
+
+    def host_arrays(self) -> Optional[dict]:
+        """The host mirror's arrays if it still describes this meta's fields
+        (same tensor objects), else None: the caller then reads the device."""
+        h = self.host
+        if h is None or len(h.of) != len(MIRRORED):
+            return None
+        for name, t in zip(MIRRORED, h.of):
+            if getattr(self, name) is not t:
+                return None
+        return h.arrays
 
     @property
     def n_seqs(self) -> int:

@@ -43,7 +43,7 @@ class BlockAllocator:
         self._bs = block_size
         self._watermark = watermark_blocks
         self._free: deque[int] = deque(range(num_blocks))
-        self._rc: list[int] = [0] * num_blocks
+        self._refcount: list[int] = [0] * num_blocks
         self.total_allocated = 0
         self.total_freed = 0
         self.peak_used = 0
@@ -60,7 +60,7 @@ class BlockAllocator:
 
     def refcount(self, block_id: int) -> int:
         self._check_id(block_id)
-        return self._rc[block_id]
+        return self._refcount[block_id]
 
     def tokens_capacity(self) -> int:
         return self._n * self._bs
@@ -84,8 +84,8 @@ class BlockAllocator:
             )
         got = [self._free.popleft() for _ in range(n_blocks)]
         for b in got:
-            assert self._rc[b] == 0, f"Block {b} on the free list has refcount {self._rc[b]}"
-            self._rc[b] = 1
+            assert self._refcount[b] == 0, f"Block {b} on the free list has refcount {self._refcount[b]}"
+            self._refcount[b] = 1
         self.total_allocated += n_blocks
         self.peak_used = max(self.peak_used, self.num_used)
         return got
@@ -93,18 +93,20 @@ class BlockAllocator:
     def incref(self, block_ids: Iterable[int]) -> None:
         for b in block_ids:
             self._check_id(b)
-            if self._rc[b] == 0:
-                raise AllocationError(f"Cannot incref block {b}: it is free (refcount 0)")
-            self._rc[b] += 1
+            if self._refcount[b] == 0:
+                raise AllocationError(
+                    f"Cannot incref block {b}: its refcount is 0, so it sits on the free list "
+                    "and its contents belong to nobody")
+            self._refcount[b] += 1
 
     def free(self, block_ids: Sequence[int]) -> None:
         """Drop one reference per id; an id returns to the BACK of the free list at 0."""
         for b in block_ids:
             self._check_id(b)
-            if self._rc[b] == 0:
+            if self._refcount[b] == 0:
                 raise AllocationError(f"Double free of block {b}: refcount is already 0")
-            self._rc[b] -= 1
-            if self._rc[b] == 0:
+            self._refcount[b] -= 1
+            if self._refcount[b] == 0:
                 self._free.append(b)
                 self.total_freed += 1
 
@@ -116,17 +118,21 @@ class BlockAllocator:
             for b in free_ids:
                 (dup if b in seen else seen).add(b)
             raise AssertionError(f"Free list contains duplicates: {sorted(dup)}")
-        for b, rc in enumerate(self._rc):
+        for b, rc in enumerate(self._refcount):
             if rc < 0:
                 raise AssertionError(f"Block {b} has negative refcount {rc}")
             if rc == 0 and b not in free_set:
-                raise AssertionError(f"Block {b} has refcount 0 but is not on the free list")
+                raise AssertionError(
+                    f"Block {b} has refcount 0 but is not on the free list: it leaked "
+                    "(the pool silently lost capacity)")
             if rc > 0 and b in free_set:
-                raise AssertionError(f"Block {b} has refcount {rc} but IS on the free list")
+                raise AssertionError(
+                    f"Block {b} has refcount {rc} but IS on the free list: the next "
+                    "allocation would hand a live block to a second owner")
 
     def reset(self) -> None:
         self._free = deque(range(self._n))
-        self._rc = [0] * self._n
+        self._refcount = [0] * self._n
 
     def _check_id(self, block_id: int) -> None:
         if not 0 <= block_id < self._n:

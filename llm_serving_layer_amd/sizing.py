@@ -10,11 +10,11 @@ that change on this device.
   (sizing.py:98-101).
 * **The decode workspace is charged to the pool budget.** The split-K decode
   keeps partial outputs for every partition of a split sequence, so its
-  workspace grows with the pages a batch can reference, i.e. with the pool.
-  The plan reserves the worst case for a pool of ``num_blocks`` blocks and a
-  batch of up to ``max_batch_seqs`` sequences, using the library's own
-  ``pkv_decode_workspace_bytes``, and picks the largest ``num_blocks`` for
-  which pool + workspace fit: one block more would not.
+  workspace grows with the batch: at most ``max_batch_seqs`` sequences of at
+  most ``max_seq_len`` tokens each (shared prefix blocks count once per
+  sequence that reads them). The plan reserves that worst case with the
+  library's own ``pkv_decode_workspace_bytes`` and picks the largest
+  ``num_blocks`` for which pool + workspace fit: one block more would not.
 
 The pool itself is one allocation ``[num_layers, 2, num_blocks, block_size,
 n_kv_heads, head_dim]`` (``MI355XBackend``), so ``bytes_per_block`` is also
@@ -32,7 +32,7 @@ from collections.abc import Sequence
 from dataclasses import dataclass, field
 
 __all__ = ["SizingError", "ModelKVShape", "LLAMA_3_2_1B", "KVPoolPlan", "kv_bytes_per_token",
-           "block_bytes", "decode_workspace_bound", "measure_free_hbm", "plan_kv_pool",
+           "block_bytes", "decode_workspace_bound", "decode_workspace_slots", "measure_free_hbm", "plan_kv_pool",
            "MI355X_HBM_BYTES", "LLAMA_3_2_1B_FP16_WEIGHT_BYTES",
            "DEFAULT_ACTIVATION_HEADROOM_BYTES", "DEFAULT_BLOCK_SIZE"]
 
@@ -51,6 +51,9 @@ DEFAULT_BLOCK_SIZE = 16
 #: Largest batch the decode workspace is reserved for by default: the
 #: 4096-sequence capacity workload.
 DEFAULT_MAX_BATCH_SEQS = 4096
+#: Longest sequence the decode workspace is reserved for by default (the
+#: reference's max_seq, bench/capacity.py:196-242).
+DEFAULT_MAX_SEQ_LEN = 2048
 
 
 class SizingError(ValueError):
@@ -98,30 +101,61 @@ def block_bytes(block_size: int = DEFAULT_BLOCK_SIZE, n_layers: int = 16, n_kv_h
     return block_size * kv_bytes_per_token(n_layers, n_kv_heads, head_dim, dtype_bytes)
 
 
-def decode_workspace_bound(num_blocks: int, max_batch_seqs: int, n_heads: int,
-                           n_kv_heads: int, head_dim: int, part_pages: int) -> int:
+def decode_workspace_slots(num_blocks: int, max_batch_seqs: int, part_pages: int,
+                           max_seq_len: int = DEFAULT_MAX_SEQ_LEN,
+                           block_size: int = DEFAULT_BLOCK_SIZE,
+                           shared_blocks: bool = True) -> int:
     """
-    Largest decode workspace any batch of at most ``max_batch_seqs``
-    sequences over a pool of ``num_blocks`` blocks can need.
+    Most split-K partial slots one decode batch can need.
 
     A sequence of p pages is cut into ceil(p / part_pages) partitions and
-    needs a partial slot per partition only when p > part_pages; then
-    ceil(p / part_pages) <= 2 p / part_pages, and the pages of one batch are
-    distinct blocks, so the slots of a batch number at most
-    floor(2 num_blocks / part_pages). The byte count is the library's
+    takes one partial slot per partition only when p > part_pages, so a
+    sequence of at most ``max_seq_len`` tokens takes at most
+    ceil(ceil(max_seq_len / block_size) / part_pages) slots, and a batch of
+    ``max_batch_seqs`` sequences that many times over. This holds whatever
+    the pages are: a radix prefix cache lets every sequence of a batch share
+    the same prefix blocks (serving/cache/radix.py:423-451), so the pages a
+    batch references are not bounded by the pool.
+
+    Only when no block is shared (``shared_blocks=False``) is the pool a
+    second bound: the pages of the batch are then distinct blocks, a split
+    sequence needs ceil(p / part_pages) <= 2 p / part_pages slots, and the
+    batch at most floor(2 num_blocks / part_pages); the smaller bound holds.
+    """
+    if part_pages <= 0:
+        raise SizingError(f"part_pages must be positive, got {part_pages}")
+    if max_batch_seqs <= 0:
+        raise SizingError(f"max_batch_seqs must be positive, got {max_batch_seqs}")
+    if max_seq_len <= 0 or block_size <= 0:
+        raise SizingError(f"max_seq_len ({max_seq_len}) and block_size ({block_size}) must "
+                          "be positive")
+    pages = -(-max_seq_len // block_size)
+    per_seq = -(-pages // part_pages) if pages > part_pages else 0
+    slots = max_batch_seqs * per_seq
+    if not shared_blocks:
+        slots = min(slots, (2 * num_blocks) // part_pages)
+    return slots
+
+
+def decode_workspace_bound(num_blocks: int, max_batch_seqs: int, n_heads: int,
+                           n_kv_heads: int, head_dim: int, part_pages: int,
+                           max_seq_len: int = DEFAULT_MAX_SEQ_LEN,
+                           block_size: int = DEFAULT_BLOCK_SIZE,
+                           shared_blocks: bool = True) -> int:
+    """
+    Largest decode workspace any batch of at most ``max_batch_seqs``
+    sequences of at most ``max_seq_len`` tokens can need
+    (``decode_workspace_slots`` slots). The byte count is the library's
     (``pkv_decode_workspace_bytes``), so it cannot drift from what the
     backend allocates.
     """
     from . import _native
 
-    if part_pages <= 0:
-        raise SizingError(f"part_pages must be positive, got {part_pages}")
-    if max_batch_seqs <= 0:
-        raise SizingError(f"max_batch_seqs must be positive, got {max_batch_seqs}")
-    if n_heads <= 0 or n_heads % n_kv_heads:
+    if n_heads <= 0 or n_kv_heads <= 0 or n_heads % n_kv_heads:
         raise SizingError(f"n_heads ({n_heads}) must be a positive multiple of n_kv_heads "
                           f"({n_kv_heads})")
-    slots = (2 * num_blocks) // part_pages
+    slots = decode_workspace_slots(num_blocks, max_batch_seqs, part_pages, max_seq_len,
+                                   block_size, shared_blocks)
     if slots <= 0:
         return 0
     return int(_native.load().pkv_decode_workspace_bytes(max_batch_seqs, slots, n_heads,
@@ -164,6 +198,8 @@ class KVPoolPlan:
     n_heads: int = 0
     max_batch_seqs: int = 0
     part_pages: int = 0
+    max_seq_len: int = DEFAULT_MAX_SEQ_LEN
+    shared_blocks: bool = True
     measured: bool = False
     notes: list[str] = field(default_factory=list)
 
@@ -172,7 +208,8 @@ class KVPoolPlan:
             return 0
         return decode_workspace_bound(num_blocks, self.max_batch_seqs, self.n_heads,
                                       self.shape.n_kv_heads, self.shape.head_dim,
-                                      self.part_pages)
+                                      self.part_pages, self.max_seq_len, self.block_size,
+                                      self.shared_blocks)
 
     def is_self_consistent(self) -> bool:
         """``num_blocks`` blocks and their workspace fit; one block more would not."""
@@ -208,10 +245,14 @@ class KVPoolPlan:
             f"({self.available_bytes / GIB:.2f} GiB)",
         ]
         if self.max_batch_seqs:
+            slots = decode_workspace_slots(self.num_blocks, self.max_batch_seqs,
+                                           self.part_pages, self.max_seq_len, self.block_size,
+                                           self.shared_blocks)
             lines.append(
                 f"- decode workspace    {self.workspace_bytes:,} B (batches of <= "
-                f"{self.max_batch_seqs} seqs, {self.part_pages}-page partitions, "
-                f"<= {2 * self.num_blocks // self.part_pages:,} partial slots)")
+                f"{self.max_batch_seqs} seqs of <= {self.max_seq_len} tokens, "
+                f"{self.part_pages}-page partitions, <= {slots:,} partial slots"
+                f"{'' if self.shared_blocks else ', no shared blocks'})")
         lines += [
             f"num_blocks            largest n with n x {self.bytes_per_block:,} + workspace(n) "
             f"<= {self.available_bytes:,}: {self.num_blocks:,}",
@@ -259,6 +300,7 @@ def plan_kv_pool(total_vram_bytes: int | None = MI355X_HBM_BYTES,
                  block_size: int = DEFAULT_BLOCK_SIZE, shape: ModelKVShape = LLAMA_3_2_1B,
                  notes: Sequence[str] | None = None, *, n_heads: int = 32,
                  max_batch_seqs: int = DEFAULT_MAX_BATCH_SEQS, part_pages: int = 10,
+                 max_seq_len: int = DEFAULT_MAX_SEQ_LEN, shared_blocks: bool = True,
                  device="cuda:0") -> KVPoolPlan:
     """
     Size the pool from an HBM budget:
@@ -269,7 +311,10 @@ def plan_kv_pool(total_vram_bytes: int | None = MI355X_HBM_BYTES,
     ``total_vram_bytes=None`` measures the budget on ``device`` (free bytes
     now, so weights already resident should be passed as 0).
     ``max_batch_seqs=0`` reserves no decode workspace, which gives the
-    reference's floor(available / block_bytes) exactly.
+    reference's floor(available / block_bytes) exactly. The workspace is
+    reserved for batches of up to ``max_batch_seqs`` sequences of up to
+    ``max_seq_len`` tokens whose prefix blocks may be shared; pass
+    ``shared_blocks=False`` only for a deployment without a prefix cache.
     """
     notes = list(notes or [])
     measured = total_vram_bytes is None
@@ -302,7 +347,8 @@ def plan_kv_pool(total_vram_bytes: int | None = MI355X_HBM_BYTES,
         if not max_batch_seqs:
             return 0
         return decode_workspace_bound(n, max_batch_seqs, n_heads, shape.n_kv_heads,
-                                      shape.head_dim, part_pages)
+                                      shape.head_dim, part_pages, max_seq_len, block_size,
+                                      shared_blocks)
 
     # n * per_block + workspace(n) grows with n: binary search for the largest fit
     lo, hi = 0, available // per_block
@@ -329,4 +375,5 @@ def plan_kv_pool(total_vram_bytes: int | None = MI355X_HBM_BYTES,
                       bytes_used=int(used), bytes_leftover=int(available - used - ws),
                       workspace_bytes=int(ws), n_heads=int(n_heads),
                       max_batch_seqs=int(max_batch_seqs), part_pages=int(part_pages),
+                      max_seq_len=int(max_seq_len), shared_blocks=bool(shared_blocks),
                       measured=measured, notes=notes)

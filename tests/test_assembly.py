@@ -169,3 +169,24 @@ def test_dtypes_match_the_contract():
     assert meta.positions.dtype == torch.int64
     m64 = build_batch_meta([grow(SequenceBlocks(a), 4)], DEV, PAGE, dtype_index=torch.int64)
     assert m64.kv_indices.dtype == torch.int64 and m64.positions.dtype == torch.int64
+
+
+def test_host_mirror_matches_the_fields_and_dies_with_a_replaced_field():
+    """build_batch_meta keeps its host arrays on the meta (so a backend can
+    plan without reading the device back); they equal the fields, and a meta
+    rebuilt with dataclasses.replace no longer vouches for them."""
+    a = BlockAllocator(64, 16)
+    seqs = [SequenceBlocks(a, seq_id=i) for i in range(3)]
+    for s, n in zip(seqs, [5, 17, 40]):
+        s.append(n)
+    meta = build_batch_meta([ScheduledSeq(s, [0] * q) for s, q in zip(seqs, [5, 1, 3])],
+                            "cpu", 16)
+    h = meta.host_arrays()
+    assert h is not None
+    for name in ("query_lens", "cu_query_lens", "kv_lens", "kv_indptr", "kv_indices",
+                 "kv_last_page_len", "slot_mapping"):
+        assert getattr(meta, name).tolist() == h[name].tolist(), name
+    assert dataclasses.replace(meta, is_prefill=True).host_arrays() is h
+    moved = dataclasses.replace(meta, slot_mapping=meta.slot_mapping.clone())
+    assert moved.host_arrays() is None
+    assert dataclasses.replace(meta, host=None).host_arrays() is None

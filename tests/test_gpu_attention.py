@@ -381,6 +381,39 @@ def test_plan_once_per_step_and_prefill_hint_checked():
         p.gpu.attend(torch.zeros(1, 32, 64, device=DEV, dtype=torch.float16), 0, 0.125, bad)
 
 
+def test_plan_from_the_host_mirror_reads_nothing_back(monkeypatch):
+    """A meta from build_batch_meta carries its host arrays: planning it, the
+    fused append and the decode launch make no device-to-host copy. A meta
+    without the mirror falls back to one read-back (caught the same way)."""
+    print("sync-free planning", flush=True)
+    from llm_serving_layer_amd import ScheduledSeq, build_batch_meta
+
+    bk = MI355XBackend(2, 256, 16, 8, 32, 64, device=DEV)
+    a = BlockAllocator(256, 16)
+    seqs = [SequenceBlocks(a, seq_id=i) for i in range(5)]
+    for s, n in zip(seqs, [3, 40, 170, 700, 16]):
+        s.append(n)
+    meta = build_batch_meta([ScheduledSeq(s, [0]) for s in seqs], DEV, 16)
+    q = torch.randn(5, 32, 64, device=DEV).half()
+    k = torch.randn(5, 8, 64, device=DEV).half()
+
+    def no_readback(self, *args, **kwargs):
+        raise AssertionError("device-to-host copy during planning")
+
+    with monkeypatch.context() as m:
+        m.setattr(torch.Tensor, "cpu", no_readback)
+        for layer in range(2):
+            bk.append_kv(layer, k, k, meta)
+            out = bk.attend(q, layer, 0.125, meta)
+        bare = dataclasses.replace(meta, host=None)
+        with pytest.raises(AssertionError, match="device-to-host"):
+            bk.attend(q, 0, 0.125, bare)
+    assert bk.n_plans == 1
+    bk.invalidate_plan()
+    again = bk.attend(q, 1, 0.125, dataclasses.replace(meta, host=None))
+    assert torch.equal(again, out), "mirror and read-back plans must agree"
+
+
 def test_protocol_and_accounting():
     from llm_serving_layer_amd import AttentionBackend
 
@@ -535,11 +568,11 @@ def test_packed_sequence_equals_solo_bitwise():
         assert torch.equal(solo, mixed[i:i + 1]), f"seq {i}: split batch changed the bits"
 
 
-def test_mixed_batch_decodes_equal_pure_decode_bitwise():
+def test_mixed_batch_equals_solo_bitwise():
     """Prefill chunks and one-token decodes in one batch: each decode token's
     output has the same bits as the same decode run alone (the decodes of a
-    mixed batch take the decode kernel), and the whole batch matches the
-    oracle."""
+    mixed batch take the decode kernel), each prefill chunk the same bits as
+    that chunk run alone, and the whole batch matches the oracle."""
     print("mixed prefill + decode batch", flush=True)
     p = Pair(1, 256, 16, 8, 32, 64, part_pages=4)
     a = BlockAllocator(256, 16)
@@ -559,6 +592,12 @@ def test_mixed_batch_decodes_equal_pure_decode_bitwise():
         solo = p.gpu.attend(q[cu[i]:cu[i] + 1], 0, 0.125,
                             make_meta([seqs[i]], [1], 16, device=DEV))
         assert torch.equal(solo, mixed[cu[i]:cu[i] + 1]), f"decode {i} changed beside prefills"
+    # and every prefill chunk of the mixed batch equals its solo run, bitwise
+    # (the reference's batched == solo, tests/test_paged_torch.py:541-587)
+    for i, ql in ((1, 24), (3, 70)):
+        solo = p.gpu.attend(q[cu[i]:cu[i] + ql], 0, 0.125,
+                            make_meta([seqs[i]], [ql], 16, device=DEV))
+        assert torch.equal(solo, mixed[cu[i]:cu[i] + ql]), f"prefill {i} changed when batched"
 
 
 @pytest.mark.parametrize("geom", [(8, 32, 128), (2, 32, 64), (8, 8, 64)])

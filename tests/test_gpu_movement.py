@@ -16,7 +16,8 @@ import torch
 from llm_serving_layer_amd import BlockAllocator, SequenceBlocks
 from llm_serving_layer_amd.backend import MI355XBackend
 from llm_serving_layer_amd.swap import KVSwapSpace, SwapSpaceFull
-from oracle import append_closed_form, copy_blocks_closed_form
+from oracle import (append_closed_form, copy_blocks_closed_form, gather_closed_form,
+                    scatter_closed_form)
 
 from ._util import make_meta
 
@@ -217,7 +218,9 @@ def test_swap_checks_and_budget():
 
 
 def test_swap_bulk_bit_exact():
-    """64 sequences x 16 blocks at full geometry, scattered ids, bit-exact."""
+    """64 sequences x 16 blocks at full geometry, scattered ids, bit-exact:
+    the host buffers against the oracle's gather (logical block order), the
+    pool after swap-in against its scatter into the new blocks."""
     print("swap bulk 64x16 blocks, 16 layers", flush=True)
     bk = backend(num_layers=16, num_blocks=2200, dtype=torch.float16)
     poison(bk, 9)
@@ -229,7 +232,9 @@ def test_swap_bulk_bit_exact():
     src = SequenceBlocks(a, seq_id=0)
     src.append(1024 * 16)
     assert src.block_ids == out_ids
-    want = bk._pool[:, :, out_ids].clone()
+    pools = bk._pool.cpu().numpy()                       # (L, 2, NB, bs, Hkv, d)
+    want_k = gather_closed_form([pools[l, 0] for l in range(16)], out_ids)
+    want_v = gather_closed_form([pools[l, 1] for l in range(16)], out_ids)
     swap = KVSwapSpace(bk)
     h = swap.swap_out("big", src)
     a.free(in_ids)
@@ -237,7 +242,13 @@ def test_swap_bulk_bit_exact():
     dst = SequenceBlocks(a, seq_id=1)
     dst.append(1024 * 16)
     assert dst.block_ids == in_ids
+    swap.synchronize()
+    assert np.array_equal(h.k.numpy(), want_k) and np.array_equal(h.v.numpy(), want_v)
     swap.swap_in(h, dst)
     torch.cuda.synchronize()
-    assert torch.equal(bk._pool[:, :, in_ids], want)
+    after = bk._pool.cpu().numpy()
+    exp_k = scatter_closed_form([pools[l, 0] for l in range(16)], want_k, in_ids)
+    exp_v = scatter_closed_form([pools[l, 1] for l in range(16)], want_v, in_ids)
+    for l in range(16):
+        assert np.array_equal(after[l, 0], exp_k[l]) and np.array_equal(after[l, 1], exp_v[l]), l
     swap.release(h)

@@ -28,7 +28,8 @@ import pytest
 import torch
 
 from llm_serving_layer_amd import BlockAllocator, SequenceBlocks
-from oracle import PagedTorchOracle, copy_blocks_closed_form, naive_attention
+from oracle import (PagedTorchOracle, append_closed_form, copy_blocks_closed_form,
+                    gather_closed_form, naive_attention, scatter_closed_form)
 
 from ._util import make_meta
 
@@ -133,6 +134,79 @@ def test_layers_independent_and_copy_block_all_layers():
         assert np.array_equal(bk.v_pool[layer].numpy(), want_v[layer])
     with pytest.raises(IndexError):
         bk.copy_block(0, 8)
+
+
+def _encoded_pools(n_layers=3, nb=10, bs=4, hkv=2, d=3, offset=0.0):
+    """Every element of block b of layer l holds 1000 l + b + offset, so a
+    wrong layer, a wrong block or a transposed index shows in the values."""
+    return [np.broadcast_to((1000.0 * l + np.arange(nb) + offset)[:, None, None, None],
+                            (nb, bs, hkv, d)).copy() for l in range(n_layers)]
+
+
+def test_swap_gather_closed_form_known_answer():
+    """The swap-out copy (serving/scheduler/preemption.py:490-509) keeps a
+    victim's blocks in LOGICAL order: host[l, i] is block ids[i] of layer l,
+    shaped (L, n, bs, Hkv, d) (preemption.py:303-332)."""
+    pools = _encoded_pools()
+    ids = [7, 2, 9, 2, 0]          # scattered, descending runs, a repeat
+    host = gather_closed_form(pools, ids)
+    assert host.shape == (3, 5, 4, 2, 3)
+    for l in range(3):
+        for i, b in enumerate(ids):
+            assert np.all(host[l, i] == 1000.0 * l + b), (l, i)
+    assert gather_closed_form(pools, []).shape[1] == 0
+
+
+def test_swap_scatter_closed_form_known_answer_and_round_trip():
+    """The swap-in copy (preemption.py:511-523): block ids[i] of layer l
+    receives host[l, i]; no other block changes. A gather from one set of
+    blocks scattered into another set reproduces the victim's KV there."""
+    pools = _encoded_pools()
+    host = np.stack([np.broadcast_to((-1.0 - 100.0 * l - np.arange(3))[:, None, None, None],
+                                     (3, 4, 2, 3)) for l in range(3)])
+    ids = [8, 1, 5]
+    out = scatter_closed_form(pools, host, ids)
+    for l in range(3):
+        for b in range(10):
+            if b in ids:
+                assert np.all(out[l][b] == -1.0 - 100.0 * l - ids.index(b))
+            else:
+                assert np.all(out[l][b] == pools[l][b]), (l, b)
+        assert np.all(pools[l] == _encoded_pools()[l]), "scatter must not modify its input"
+    src, dst = [4, 0, 6], [9, 3, 2]
+    moved = scatter_closed_form(pools, gather_closed_form(pools, src), dst)
+    for l in range(3):
+        for s_, d_ in zip(src, dst):
+            assert np.array_equal(moved[l][d_], pools[l][s_])
+
+
+def test_planted_swap_mistakes_fail_the_known_answers():
+    pools = _encoded_pools()
+    ids = [7, 2, 9]
+    want = gather_closed_form(pools, ids)
+    wrong_order = np.stack([p[np.sort(ids)] for p in pools])        # physical, not logical
+    wrong_layer = np.stack([pools[0][ids] for _ in pools])          # layer index dropped
+    assert not np.array_equal(want, wrong_order)
+    assert not np.array_equal(want, wrong_layer)
+
+
+def test_append_and_copy_closed_forms_known_answers():
+    """append: flat slot s = block * bs + row receives token t's row
+    (paged_torch.py:270-276); copy: every layer, K and V, dst = src, pair by
+    pair, src == dst a no-op (paged_torch.py:181-207)."""
+    pool = _encoded_pools(n_layers=1)[0]
+    x = -np.arange(2 * 2 * 3, dtype=np.float64).reshape(2, 2, 3) - 1
+    got = append_closed_form(pool, x, [4 * 6 + 1, 4 * 9 + 3])
+    assert np.array_equal(got[6, 1], x[0]) and np.array_equal(got[9, 3], x[1])
+    mask = np.ones(got.shape[:2], bool)
+    mask[6, 1] = mask[9, 3] = False
+    assert np.array_equal(got[mask], pool[mask])
+    ks, vs = _encoded_pools(), _encoded_pools(offset=0.5)
+    ck, cv = copy_blocks_closed_form(ks, vs, [(1, 4), (3, 3), (4, 8)])
+    for l in range(3):
+        assert np.all(ck[l][4] == 1000.0 * l + 1) and np.all(cv[l][4] == 1000.0 * l + 1.5)
+        assert np.all(ck[l][8] == 1000.0 * l + 1), "pairs apply in order: 4 was already 1"
+        assert np.all(ck[l][3] == 1000.0 * l + 3)
 
 
 # ----------------------------------------------------------- vs textbook

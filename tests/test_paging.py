@@ -50,16 +50,28 @@ def test_incref_and_shared_free():
     assert a.refcount(b[0]) == 1 and a.num_free == 3
     a.free(b)
     assert a.num_free == 4
-    with pytest.raises(AllocationError):
+    with pytest.raises(AllocationError, match="refcount is 0"):
         a.incref(b)
 
 
 def test_check_invariants_detects_corruption():
+    """The reference's allocator tests corrupt the private state directly and
+    match these fragments (tests/test_allocator.py:300-366)."""
     a = BlockAllocator(4, 16)
     a.allocate(2)
-    a._rc[0] = 0  # leaked: refcount 0 but not free
-    with pytest.raises(AssertionError, match="not on the free list"):
+    a._refcount[0] = 0  # leaked: refcount 0 but not free
+    with pytest.raises(AssertionError, match="leaked"):
         a.check_invariants()
+    b = BlockAllocator(4, 16)
+    (x,) = b.allocate(1)
+    b._free.append(x)  # live AND free
+    with pytest.raises(AssertionError, match="second owner"):
+        b.check_invariants()
+    c = BlockAllocator(4, 16)
+    (y,) = c.allocate(1)
+    c.free([y])
+    with pytest.raises(AllocationError, match="refcount is 0"):
+        c.incref([y])
 
 
 def test_slot_for_scattered_blocks():

@@ -17,7 +17,8 @@ import pytest
 from llm_serving_layer_amd import _native
 from llm_serving_layer_amd.sizing import (LLAMA_3_2_1B, MI355X_HBM_BYTES, SizingError,
                                           block_bytes, decode_workspace_bound,
-                                          kv_bytes_per_token, plan_kv_pool)
+                                          decode_workspace_slots, kv_bytes_per_token,
+                                          plan_kv_pool)
 
 KIB, MIB, GIB = 1024, 1024**2, 1024**3
 
@@ -138,8 +139,30 @@ def test_workspace_bound_covers_every_batch_the_pool_can_hold(part_pages):
         pages, slots = _plan_slots(lens, part_pages)
         assert pages <= num_blocks
         need = _native.load().pkv_decode_workspace_bytes(len(lens), max(slots, 1), 32, 8, 64)
-        assert need <= decode_workspace_bound(num_blocks, max(len(lens), 1), 32, 8, 64,
-                                              part_pages)
+        for shared in (False, True):  # distinct blocks: both bounds hold
+            assert need <= decode_workspace_bound(num_blocks, max(len(lens), 1), 32, 8, 64,
+                                                  part_pages, max_seq_len=max(lens),
+                                                  shared_blocks=shared)
+
+
+@pytest.mark.parametrize("part_pages", [3, 10, 64])
+def test_workspace_bound_holds_under_radix_prefix_sharing(part_pages):
+    """64 sequences share one 120-page prefix (refcounted blocks, as the radix
+    cache shares them) and own one page each: the batch references 7744
+    pages of a 200-block pool. The slots the library's plan really takes
+    exceed the distinct-block bound floor(2 N / part_pages), and stay within
+    the bound reserved for shared blocks."""
+    num_blocks, n = 200, 64
+    lens = [120 * 16 + 1 + i % 16 for i in range(n)]      # 121 pages, <= 2048 tokens
+    pages, slots = _plan_slots(lens, part_pages)
+    assert pages == n * 121 > num_blocks
+    need = _native.load().pkv_decode_workspace_bytes(n, slots, 32, 8, 64)
+    distinct = decode_workspace_bound(num_blocks, n, 32, 8, 64, part_pages,
+                                      shared_blocks=False)
+    shared = decode_workspace_bound(num_blocks, n, 32, 8, 64, part_pages)
+    assert need > distinct, "the distinct-block bound must not be used with sharing"
+    assert need <= shared
+    assert decode_workspace_slots(num_blocks, n, part_pages) >= slots
 
 
 def test_derivation_is_printable_and_shows_the_arithmetic():
