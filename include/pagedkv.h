@@ -143,6 +143,33 @@ int pkv_attend_decode(const void* q, void* out,
                       int32_t* status_word, void* stream);
 
 /*
+ * No-allocation decode — no counterpart in the reference. For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): the same launch as
+ * pkv_attend_decode, same arguments without the workspace. The split-K
+ * workspace is a file-scope device array of PKV_DECODE_SCRATCH_BYTES on each
+ * GPU the library runs on (held until the process ends); a plan whose
+ * pkv_decode_workspace_bytes exceeds it is rejected with PKV_ERR_CAPACITY.
+ * Allocates nothing: no hipMalloc, hipFree or allocating library call. The
+ * arrival counters are cleared by a fill kernel on `stream` before each launch.
+ * Every call on one GPU shares that GPU's array, so calls that overlap in
+ * time on one GPU (different streams, or threads) race; calls in order on one
+ * stream do not.
+ */
+#define PKV_DECODE_SCRATCH_BYTES (64LL * 1024 * 1024)
+
+int pkv_attend_decode_noalloc(const void* q, void* out,
+                              void* k_pool, void* v_pool, int64_t num_blocks,
+                              const int32_t* kv_indptr, const int32_t* kv_indices,
+                              const int32_t* kv_lens, int32_t n_seqs,
+                              int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                              int32_t page_size, float scale, int32_t dtype,
+                              const int32_t* plan, int32_t n_work, int32_t n_slots,
+                              int32_t part_pages,
+                              const void* k_new, const void* v_new, const int32_t* slot_mapping,
+                              int32_t* status_word, void* stream);
+
+/*
  * Prefill plan (host function) — tiles each sequence's query rows for
  * pkv_attend_prefill. Output `plan` = n_tiles items {seq, q_start, q_len,
  * 0}, ordered by descending work.

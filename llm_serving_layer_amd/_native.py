@@ -15,9 +15,10 @@ from pathlib import Path
 # PKV_LIBRARY selects another build of the same library (e.g. a tuning variant).
 LIB_PATH = Path(os.environ.get("PKV_LIBRARY") or
                 Path(__file__).resolve().parent / "_native" / "libpagedkv.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
+DECODE_SCRATCH_BYTES = 64 * 1024 * 1024   # PKV_DECODE_SCRATCH_BYTES
 OK, ERR_INVALID, ERR_RANGE, ERR_HIP, ERR_CAPACITY = 0, 1, 2, 3, 4
 STATUS_BAD_SLOT, STATUS_BAD_PAGE, STATUS_BAD_BLOCK = 1, 2, 4
 
@@ -34,6 +35,9 @@ SIGNATURES = {
     "pkv_attend_decode": (C.c_int, [_p, _p, _p, _p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32,
                                     _i32, _f32, _i32, _p, _i32, _i32, _i32, _p, _p, _p, _p,
                                     _i64, _p, _p]),
+    "pkv_attend_decode_noalloc": (C.c_int, [_p, _p, _p, _p, _i64, _p, _p, _p, _i32, _i32, _i32,
+                                            _i32, _i32, _f32, _i32, _p, _i32, _i32, _i32, _p,
+                                            _p, _p, _p, _p]),
     "pkv_plan_prefill": (C.c_int, [_p, _p, _p, _p, _i32, _i32, _i32, _p, _i64, _p]),
     "pkv_prefill_q_tile": (C.c_int, [_i32, _i32, _i32, _i32, _i32]),
     "pkv_attend_prefill": (C.c_int, [_p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _i32, _i32,

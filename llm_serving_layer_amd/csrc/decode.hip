@@ -60,6 +60,7 @@
 // exactly "append, then attend" (the caller guarantees that no other
 // sequence of the launch reads that slot).
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "mfma.h"
@@ -778,16 +779,26 @@ extern "C" int64_t pkv_decode_workspace_bytes(int32_t n_seqs, int32_t n_slots,
   return counters + (po + (int64_t)n_slots * n_heads * 2) * 4;
 }
 
-extern "C" int pkv_attend_decode(const void* q, void* out, void* k_pool, void* v_pool,
-                                 int64_t num_blocks, const int32_t* kv_indptr,
-                                 const int32_t* kv_indices, const int32_t* kv_lens,
-                                 int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads,
-                                 int32_t head_dim, int32_t page_size, float scale,
-                                 int32_t dtype, const int32_t* plan, int32_t n_work,
-                                 int32_t n_slots, int32_t part_pages, const void* k_new,
-                                 const void* v_new, const int32_t* slot_mapping,
-                                 void* workspace, int64_t workspace_bytes,
-                                 int32_t* status_word, void* stream) {
+namespace pkv {
+
+// The decode launch shared by both entry points. `zero_counters` clears the
+// arrival counters at the front of the workspace with a fill kernel first
+// (kept to a kernel, not a memset, so the call can sit inside a captured
+// graph).
+__global__ void zero_words(int32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+static int attend_decode(const void* q, void* out, void* k_pool, void* v_pool,
+                         int64_t num_blocks, const int32_t* kv_indptr,
+                         const int32_t* kv_indices, const int32_t* kv_lens, int32_t n_seqs,
+                         int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                         int32_t page_size, float scale, int32_t dtype, const int32_t* plan,
+                         int32_t n_work, int32_t n_slots, int32_t part_pages, const void* k_new,
+                         const void* v_new, const int32_t* slot_mapping, void* workspace,
+                         int64_t workspace_bytes, bool zero_counters, int32_t* status_word,
+                         void* stream) {
   int rc = check_geometry(n_heads, n_kv_heads, head_dim, page_size, dtype);
   if (rc) return rc;
   if (n_seqs <= 0) return PKV_OK;
@@ -830,6 +841,12 @@ extern "C" int pkv_attend_decode(const void* q, void* out, void* k_pool, void* v
     pml = po + pf;
     o_bytes = (uint32_t)(pf * 4);
     ml_bytes = (uint32_t)(mlf * 4);
+    if (zero_counters) {
+      const int64_t words = (int64_t)n_seqs * n_kv_heads;
+      hipLaunchKernelGGL(zero_words, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s,
+                         cnt, words);
+      PKV_LAUNCH_CHECK();
+    }
   }
   // A plan without partial slots splits no sequence; its partitions are packs
   // of whole consecutive sequences (pkv_plan_decode).
@@ -838,4 +855,85 @@ extern "C" int pkv_attend_decode(const void* q, void* out, void* k_pool, void* v
      cnt, status_word, s);
   PKV_LAUNCH_CHECK();
   return PKV_OK;
+}
+
+// Workspace of the no-allocation entry point: one file-scope device array,
+// which every GPU the library runs on holds (at its own address) until the
+// process ends. In host code `scratch` names a host-side stand-in, never the
+// device memory: the device address is looked up once per device with
+// hipGetSymbolAddress and only that address is passed to kernels.
+static __device__ __align__(256) unsigned char scratch[PKV_DECODE_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// This device's address of `scratch`, looked up on the first call on the
+// device (with it current); nullptr with the error set on failure.
+static void* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(PKV_ERR_HIP, "no current HIP device (or device index above %d)", kMaxDevices - 1);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      fail(PKV_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+           hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace pkv
+
+extern "C" int pkv_attend_decode(const void* q, void* out, void* k_pool, void* v_pool,
+                                 int64_t num_blocks, const int32_t* kv_indptr,
+                                 const int32_t* kv_indices, const int32_t* kv_lens,
+                                 int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, int32_t page_size, float scale,
+                                 int32_t dtype, const int32_t* plan, int32_t n_work,
+                                 int32_t n_slots, int32_t part_pages, const void* k_new,
+                                 const void* v_new, const int32_t* slot_mapping,
+                                 void* workspace, int64_t workspace_bytes,
+                                 int32_t* status_word, void* stream) {
+  return attend_decode(q, out, k_pool, v_pool, num_blocks, kv_indptr, kv_indices, kv_lens,
+                       n_seqs, n_heads, n_kv_heads, head_dim, page_size, scale, dtype, plan,
+                       n_work, n_slots, part_pages, k_new, v_new, slot_mapping, workspace,
+                       workspace_bytes, false, status_word, stream);
+}
+
+extern "C" int pkv_attend_decode_noalloc(const void* q, void* out, void* k_pool, void* v_pool,
+                                         int64_t num_blocks, const int32_t* kv_indptr,
+                                         const int32_t* kv_indices, const int32_t* kv_lens,
+                                         int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads,
+                                         int32_t head_dim, int32_t page_size, float scale,
+                                         int32_t dtype, const int32_t* plan, int32_t n_work,
+                                         int32_t n_slots, int32_t part_pages,
+                                         const void* k_new, const void* v_new,
+                                         const int32_t* slot_mapping, int32_t* status_word,
+                                         void* stream) {
+  void* ws = nullptr;
+  if (n_slots > 0) {
+    const int64_t need =
+        pkv_decode_workspace_bytes(n_seqs, n_slots, n_heads, n_kv_heads, head_dim);
+    if (need <= 0)
+      return fail(PKV_ERR_INVALID, "invalid geometry for a split-K plan");
+    if (need > (int64_t)PKV_DECODE_SCRATCH_BYTES)
+      return fail(PKV_ERR_CAPACITY, "split-K plan needs %lld workspace bytes; the "
+                  "no-allocation entry point holds at most %lld (use pkv_attend_decode with a "
+                  "workspace, or larger partitions)", (long long)need,
+                  (long long)PKV_DECODE_SCRATCH_BYTES);
+    ws = scratch_on_current_device();
+    if (!ws) return PKV_ERR_HIP;
+  }
+  return attend_decode(q, out, k_pool, v_pool, num_blocks, kv_indptr, kv_indices, kv_lens,
+                       n_seqs, n_heads, n_kv_heads, head_dim, page_size, scale, dtype, plan,
+                       n_work, n_slots, part_pages, k_new, v_new, slot_mapping, ws,
+                       (int64_t)PKV_DECODE_SCRATCH_BYTES, true, status_word, stream);
 }
