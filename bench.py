@@ -356,7 +356,7 @@ def bench_decode(args):
                          "inside the loop")},
         "parity": r["parity"],
         "roofline": {
-            "kernel": "pkv::decode_kernel<_Float16,64,4,1,false> (split-K partitions, KV append fused), one launch per layer",
+            "kernel": "pkv::decode_kernel<_Float16,64,4> (LPT bins of (sequence, piece) items, split-K merge by the last arriver, KV append fused), one launch per layer",
             "bound": "hbm", "achieved": round(r["kern_gbps"], 1), "peak": PEAK_HBM_GBPS,
             "unit": "GB/s", "frac": round(r["kern_gbps"] / PEAK_HBM_GBPS, 4),
             "traffic": traffic_for("decode_kernel_batch256"),

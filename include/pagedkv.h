@@ -70,34 +70,50 @@ int pkv_append_kv(void* k_pool, void* v_pool, int64_t num_slots,
  * Decode plan (host function, synchronous, no device access) — the
  * counterpart of the reference fast path's plan step
  * (serving/backends/flashinfer_backend.py:566-676), computed once per batch
- * and reused by every layer. Splits each sequence's pages into partitions of
- * at most `part_pages` pages (split-K over the KV axis; the split depends
- * only on that sequence's own length) and orders the partitions longest
- * first. Checks that every sequence has ceil(kv_len / page_size) pages and
- * that kv_last_page_len agrees (PKV_ERR_INVALID, message naming
- * kv_last_page_len, as serving/backends/paged_torch.py:379-392 does).
+ * and reused by every layer. Checks that every sequence has
+ * ceil(kv_len / page_size) pages and that kv_last_page_len agrees
+ * (PKV_ERR_INVALID, message naming kv_last_page_len, as
+ * serving/backends/paged_torch.py:379-392 does).
  *
- * Output `plan` (int32), 8 entries per partition:
- *   {seq, index of its first page in kv_indices, n_pages, partial slot
- *    (-1: the partition is the whole sequence), kv_len, first token,
- *    n_partitions of the sequence, first slot of the sequence}
- * *n_slots_out: partial-result slots of split sequences (workspace size).
- * When no sequence is split (*n_slots_out == 0), each partition is instead a
- * pack of up to 16 whole consecutive sequences, at most `part_pages` pages
- * together: {first seq, index of its first page in kv_indices, n_pages, -1,
- * n_seqs in the pack, 0, 1, -1}. pkv_attend_decode reads a plan with
- * n_slots == 0 as packs.
+ * Each sequence of np pages is cut into ceil(np / part_pages) pieces of
+ * nearly equal size (a function of its own length only); the pieces are
+ * dealt longest first to the least-loaded of at most
+ * max_workgroups / (n_kv_heads / heads-per-workgroup) bins. The plan is
+ * bins blocks of *plan_stride_out ints: {n_items, n_pages, 0, 0}, n_pages
+ * page words (kv_indices entries, with the page's live row count - 1 in bits
+ * 27..30 and an out-of-range flag in bit 31, padded to a multiple of 4),
+ * then n_items items {seq, n_pages, first token, kv_len, partial slot (-1: a
+ * whole sequence), pieces of the sequence, its first slot, flags (bit 0: the
+ * piece holds the sequence's last page)} -- pieces of cut sequences before
+ * their last, whole sequences, then the last pieces; then 64 zero ints.
+ * *plan_needed (if not NULL) receives the ints required; a plan larger than
+ * plan_capacity returns PKV_ERR_CAPACITY and writes nothing else.
+ * *n_work_out is the grid size (workgroups), *n_slots_out the partial slots
+ * (workspace size). num_blocks must not exceed 2^27.
  */
-int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_lens,
-                    const int32_t* kv_last_page_len, int32_t n_seqs,
-                    int32_t page_size, int32_t part_pages,
-                    int32_t* plan, int64_t plan_capacity,
-                    int32_t* n_work_out, int32_t* n_slots_out);
+int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_indices,
+                    const int32_t* kv_lens, const int32_t* kv_last_page_len,
+                    int32_t n_seqs, int32_t page_size, int64_t num_blocks,
+                    int32_t n_kv_heads, int32_t part_pages, int32_t max_workgroups,
+                    int32_t* plan, int64_t plan_capacity, int64_t* plan_needed,
+                    int32_t* n_work_out, int32_t* n_slots_out, int32_t* plan_stride_out);
+
+/*
+ * Workgroups a decode plan should be dealt into on the current device: the
+ * device's compute units times the fast decode kernel's resident workgroups
+ * per compute unit for this geometry, capped at per_cu. 0 if the geometry has
+ * no fast kernel (or no device is current). No reference counterpart: it is
+ * the grid-size half of the plan step FlashInfer's plan performs internally
+ * (serving/backends/flashinfer_backend.py:658-670).
+ */
+int pkv_decode_workgroups(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                          int32_t dtype, int32_t per_cu);
 
 /*
  * Bytes of workspace pkv_attend_decode needs: arrival counters for
  * n_seqs * n_kv_heads (zero before the first launch that uses the workspace;
- * every launch leaves them zero) then n_slots partial results.
+ * every launch leaves them zero) then n_slots partial results. 0 when
+ * n_slots is 0 (no sequence is cut; no workspace is read).
  */
 int64_t pkv_decode_workspace_bytes(int32_t n_seqs, int32_t n_slots, int32_t n_heads,
                                    int32_t n_kv_heads, int32_t head_dim);
@@ -117,9 +133,10 @@ int pkv_decode_fast_path(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
  * (token i belongs to sequence i). q, out: [n_seqs, n_heads, head_dim];
  * query head h reads KV head h / (n_heads / n_kv_heads); no mask (the
  * single query is the last position). `plan` is the device copy of
- * pkv_plan_decode's output. Split sequences merge inside the launch through
- * `workspace` (256-byte aligned, pkv_decode_workspace_bytes long); launches
- * that share a workspace must not overlap in time (same stream is fine).
+ * pkv_plan_decode's output, with its n_work, n_slots and plan_stride. Cut
+ * sequences merge inside the launch through `workspace` (256-byte aligned,
+ * pkv_decode_workspace_bytes long); launches that share a workspace must not
+ * overlap in time (same stream is fine).
  *
  * Fused append: if k_new / v_new ([n_seqs, n_kv_heads, head_dim]) and
  * slot_mapping ([n_seqs]) are given, the launch also performs pkv_append_kv
@@ -128,7 +145,7 @@ int pkv_decode_fast_path(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
  *
  * Geometries outside the fast kernel (head_dim not 64/128, more than 16
  * query heads per KV head, page_size != 16, fp32) run the generic kernel,
- * which reads kv_indptr / kv_lens instead of the plan.
+ * which reads kv_indptr / kv_indices / kv_lens instead of the plan.
  */
 int pkv_attend_decode(const void* q, void* out,
                       void* k_pool, void* v_pool, int64_t num_blocks,
@@ -137,7 +154,7 @@ int pkv_attend_decode(const void* q, void* out,
                       int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                       int32_t page_size, float scale, int32_t dtype,
                       const int32_t* plan, int32_t n_work, int32_t n_slots,
-                      int32_t part_pages,
+                      int32_t plan_stride,
                       const void* k_new, const void* v_new, const int32_t* slot_mapping,
                       void* workspace, int64_t workspace_bytes,
                       int32_t* status_word, void* stream);
@@ -165,7 +182,7 @@ int pkv_attend_decode_noalloc(const void* q, void* out,
                               int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                               int32_t page_size, float scale, int32_t dtype,
                               const int32_t* plan, int32_t n_work, int32_t n_slots,
-                              int32_t part_pages,
+                              int32_t plan_stride,
                               const void* k_new, const void* v_new, const int32_t* slot_mapping,
                               int32_t* status_word, void* stream);
 

@@ -15,7 +15,7 @@ from pathlib import Path
 # PKV_LIBRARY selects another build of the same library (e.g. a tuning variant).
 LIB_PATH = Path(os.environ.get("PKV_LIBRARY") or
                 Path(__file__).resolve().parent / "_native" / "libpagedkv.so")
-ABI_VERSION = 6
+ABI_VERSION = 9
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 DECODE_SCRATCH_BYTES = 64 * 1024 * 1024   # PKV_DECODE_SCRATCH_BYTES
@@ -29,7 +29,9 @@ SIGNATURES = {
     "pkv_abi_version": (C.c_int, []),
     "pkv_last_error": (C.c_char_p, []),
     "pkv_append_kv": (C.c_int, [_p, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i32, _p, _p]),
-    "pkv_plan_decode": (C.c_int, [_p, _p, _p, _i32, _i32, _i32, _p, _i64, _p, _p]),
+    "pkv_plan_decode": (C.c_int, [_p, _p, _p, _p, _i32, _i32, _i64, _i32, _i32, _i32, _p, _i64,
+                                  _p, _p, _p, _p]),
+    "pkv_decode_workgroups": (C.c_int, [_i32, _i32, _i32, _i32, _i32]),
     "pkv_decode_workspace_bytes": (C.c_int64, [_i32, _i32, _i32, _i32, _i32]),
     "pkv_decode_fast_path": (C.c_int, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "pkv_attend_decode": (C.c_int, [_p, _p, _p, _p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32,

@@ -81,7 +81,8 @@ class _Plan:
     """Device-side metadata and launch plan for one BatchMeta (one step)."""
 
     __slots__ = ("meta", "use_prefill", "slots", "indptr", "indices", "kv_lens", "cu_q",
-                 "bidx", "plan", "n_work", "n_slots", "n_tokens", "n_seqs", "fusable", "dec")
+                 "bidx", "plan", "n_work", "n_slots", "stride", "n_tokens", "n_seqs", "fusable",
+                 "dec")
 
 
 class _DecodeRows:
@@ -89,7 +90,8 @@ class _DecodeRows:
     their token rows in q/out, and their paging metadata and decode plan as a
     batch of their own."""
 
-    __slots__ = ("rows", "indptr", "indices", "kv_lens", "plan", "n", "n_work", "n_slots")
+    __slots__ = ("rows", "indptr", "indices", "kv_lens", "plan", "n", "n_work", "n_slots",
+                 "stride")
 
 
 class _Pending:
@@ -105,7 +107,8 @@ class MI355XBackend:
                  n_heads: int, head_dim: int, device: str | torch.device = "cuda:0",
                  dtype: torch.dtype = torch.float16, *,
                  part_pages: int = DEFAULT_PART_PAGES, q_tile: int | None = None,
-                 fuse_append: bool = True):
+                 fuse_append: bool = True, decode_workgroups_per_cu: int = 2,
+                 decode_workgroups: int | None = None):
         if n_heads % n_kv_heads != 0:
             raise ValueError(
                 f"n_heads={n_heads} must be divisible by n_kv_heads={n_kv_heads}; "
@@ -125,6 +128,11 @@ class MI355XBackend:
             raise ValueError(f"q_tile={q_tile} must be positive")
         if not 1 <= part_pages <= MAX_PART_PAGES:
             raise ValueError(f"part_pages={part_pages} must be in [1, {MAX_PART_PAGES}]")
+        if decode_workgroups_per_cu < 1:
+            raise ValueError(f"decode_workgroups_per_cu={decode_workgroups_per_cu} must be "
+                             "positive")
+        if decode_workgroups is not None and decode_workgroups < 1:
+            raise ValueError(f"decode_workgroups={decode_workgroups} must be positive")
         try:
             self._lib = _native.load()
         except RuntimeError as exc:
@@ -155,6 +163,19 @@ class MI355XBackend:
         self._fast_decode = bool(self._lib.pkv_decode_fast_path(
             n_heads, n_kv_heads, head_dim, block_size, self._code, part_pages))
         self._fuse_append = fuse_append and self._fast_decode
+        # The decode grid: every bin of the plan a resident workgroup (per
+        # group of KV heads), so none waits for a slot. ``decode_workgroups``
+        # overrides the count (tests force many sequences into a bin with it).
+        self._decode_wgs = 0
+        if self._fast_decode:
+            with torch.cuda.device(self.device):
+                self._decode_wgs = int(self._lib.pkv_decode_workgroups(
+                    n_heads, n_kv_heads, head_dim, self._code, decode_workgroups_per_cu))
+            if self._decode_wgs <= 0:
+                raise RuntimeError("pkv_decode_workgroups found no resident decode workgroup "
+                                   "on this device")
+            if decode_workgroups is not None:
+                self._decode_wgs = decode_workgroups
         # A mixed batch (prefill chunks beside one-token decodes) runs its
         # decodes through the decode kernel, so a decode step's bits do not
         # depend on whether prefills share its batch.
@@ -385,7 +406,7 @@ class MI355XBackend:
         self.n_runs += 1
         if not p.use_prefill:
             self._launch_decode(q, out, kp, vp, p.indptr, p.indices, p.kv_lens, p.n_seqs,
-                                p.plan, p.n_work, p.n_slots, scale, stream,
+                                p.plan, p.n_work, p.n_slots, p.stride, scale, stream,
                                 pend if fused else None, p.slots)
         else:
             rc = self._lib.pkv_attend_prefill(
@@ -400,18 +421,19 @@ class MI355XBackend:
                 qd = q.index_select(0, d.rows)
                 od = torch.empty_like(qd)
                 self._launch_decode(qd, od, kp, vp, d.indptr, d.indices, d.kv_lens, d.n,
-                                    d.plan, d.n_work, d.n_slots, scale, stream, None, None)
+                                    d.plan, d.n_work, d.n_slots, d.stride, scale, stream, None,
+                                    None)
                 out.index_copy_(0, d.rows, od)
         return out
 
     def _launch_decode(self, q, out, kp, vp, indptr, indices, kv_lens, n_seqs, plan, n_work,
-                       n_slots, scale, stream, pend, slots) -> None:
+                       n_slots, stride, scale, stream, pend, slots) -> None:
         ws = self._workspace
         rc = self._lib.pkv_attend_decode(
             q.data_ptr(), out.data_ptr(), kp, vp, self.num_blocks, indptr.data_ptr(),
             indices.data_ptr(), kv_lens.data_ptr(), n_seqs, self.n_heads, self.n_kv_heads,
             self.head_dim, self.block_size, float(scale), self._code, plan.data_ptr(), n_work,
-            n_slots, self.part_pages, pend.k.data_ptr() if pend else None,
+            n_slots, stride, pend.k.data_ptr() if pend else None,
             pend.v.data_ptr() if pend else None, slots.data_ptr() if pend else None,
             ws.data_ptr() if ws.numel() else None, ws.numel(), self._status.data_ptr(), stream)
         _native.check(rc, "attend (decode)")
@@ -432,29 +454,29 @@ class MI355XBackend:
         with_slots = (meta.slot_mapping is not None and meta.slot_mapping.shape[0] == n
                       and meta.kv_indices.shape[0] > 0 and meta.kv_indptr.shape[0] == n + 1)
         mirror = meta.host_arrays()
+        n_pages = int(meta.kv_indices.shape[0])
         if mirror is not None:
             # the assembler's own host arrays: no device read-back
             ql, cu = mirror["query_lens"], mirror["cu_query_lens"]
             kvl, indptr = mirror["kv_lens"], mirror["kv_indptr"]
-            last = mirror["kv_last_page_len"]
+            last, indices = mirror["kv_last_page_len"], mirror["kv_indices"]
             if with_slots:
-                ix = np.clip(indptr[1:] - 1, 0, mirror["kv_indices"].shape[0] - 1)
-                last_page, new_slot = mirror["kv_indices"][ix], mirror["slot_mapping"]
+                new_slot = mirror["slot_mapping"]
         else:
             parts = [meta.query_lens, meta.cu_query_lens, meta.kv_lens, meta.kv_indptr,
-                     meta.kv_last_page_len]
-            # For the fused append: each sequence's last page id and its new slot.
+                     meta.kv_last_page_len, meta.kv_indices]
             if with_slots:
-                last_ix = (meta.kv_indptr[1:].to(torch.int64) - 1).clamp(
-                    0, meta.kv_indices.shape[0] - 1)
-                parts += [meta.kv_indices[last_ix], meta.slot_mapping]
+                parts.append(meta.slot_mapping)
             # ONE device->host transfer for everything the host plan reads.
             host = torch.cat([t.reshape(-1).to(torch.int64) for t in parts]).cpu().numpy()
             ql, cu = host[:n], host[n:2 * n + 1]
             kvl, indptr = host[2 * n + 1:3 * n + 1], host[3 * n + 1:4 * n + 2]
             last = host[4 * n + 2:5 * n + 2]
+            indices = host[5 * n + 2:5 * n + 2 + n_pages]
             if with_slots:
-                last_page, new_slot = host[5 * n + 2:6 * n + 2], host[6 * n + 2:7 * n + 2]
+                new_slot = host[5 * n + 2 + n_pages:6 * n + 2 + n_pages]
+        if with_slots:  # for the fused append: each sequence's last page id
+            last_page = indices[np.clip(indptr[1:] - 1, 0, n_pages - 1)]
         use_prefill = bool((ql > 1).any())
         if bool(meta.is_prefill) != use_prefill:
             raise ValueError(
@@ -484,8 +506,10 @@ class MI355XBackend:
         kvl32, indptr32, last32, cu32 = i32(kvl), i32(indptr), i32(last), i32(cu)
         ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
         decodes = None
+        p.stride = 0
         if not use_prefill:
-            plan, p.n_work, p.n_slots = self._plan_decode(indptr32, kvl32, last32, n)
+            plan, p.n_work, p.n_slots, p.stride = self._plan_decode(indptr32, i32(indices),
+                                                                    kvl32, last32, n)
         else:
             n_work = C.c_int32()
             cap = 4 * (int(cu[-1]) // self.q_tile + n + 1)
@@ -505,7 +529,7 @@ class MI355XBackend:
         p.kv_lens = self._dev_i32(meta.kv_lens)
         p.dec = None
         if decodes is not None:
-            p.dec = self._decode_rows(decodes, cu, indptr, kvl, last, p.indices)
+            p.dec = self._decode_rows(decodes, cu, indptr, kvl, last, indices, p.indices)
         p.cu_q = self._dev_i32(meta.cu_query_lens)
         p.bidx = self._dev_i32(meta.batch_indices)
         p.slots = (self._dev_i32(meta.slot_mapping) if meta.slot_mapping is not None
@@ -514,15 +538,25 @@ class MI355XBackend:
         self.n_plans += 1
         return p
 
-    def _plan_decode(self, indptr32, kvl32, last32, n):
-        """Host decode plan (pkv_plan_decode) plus a workspace large enough for it."""
+    def _plan_decode(self, indptr32, indices32, kvl32, last32, n):
+        """Host decode plan (pkv_plan_decode) plus a workspace large enough for it.
+        Returns (plan, n_work, n_slots, stride)."""
+        if not self._fast_decode:  # the generic kernel reads the CSR, not a plan
+            return np.zeros(4, dtype=np.int32), 1, 0, 4
         ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
-        n_work, n_slots = C.c_int32(), C.c_int32()
-        cap = 8 * (int(indptr32[-1]) + n)
-        buf = np.empty(cap, dtype=np.int32)
-        rc = self._lib.pkv_plan_decode(ptr(indptr32), ptr(kvl32), ptr(last32), n,
-                                       self.block_size, self.part_pages, ptr(buf), cap,
-                                       C.byref(n_work), C.byref(n_slots))
+        n_work, n_slots, stride = C.c_int32(), C.c_int32(), C.c_int32()
+        needed = C.c_int64()
+        cap = 6 * self._decode_wgs + 2 * int(indptr32[-1]) + 24 * n + 128
+        for _ in range(2):
+            buf = np.empty(cap, dtype=np.int32)
+            rc = self._lib.pkv_plan_decode(
+                ptr(indptr32), ptr(indices32), ptr(kvl32), ptr(last32), n, self.block_size,
+                self.num_blocks, self.n_kv_heads, self.part_pages, self._decode_wgs, ptr(buf),
+                cap, C.byref(needed), C.byref(n_work), C.byref(n_slots), C.byref(stride))
+            if rc == _native.ERR_CAPACITY and needed.value > cap:
+                cap = int(needed.value)
+                continue
+            break
         _native.check(rc, "plan (decode)")
         need = self._lib.pkv_decode_workspace_bytes(n, n_slots.value, self.n_heads,
                                                     self.n_kv_heads, self.head_dim)
@@ -533,9 +567,9 @@ class MI355XBackend:
             # a previous layout may have left partial data where counters now sit
             counter_bytes = (4 * n * self.n_kv_heads + 255) // 256 * 256
             self._workspace[:counter_bytes].zero_()
-        return buf[:8 * n_work.value].copy(), n_work.value, n_slots.value
+        return (buf[:int(needed.value)].copy(), n_work.value, n_slots.value, stride.value)
 
-    def _decode_rows(self, dec, cu, indptr, kvl, last, indices_dev) -> _DecodeRows:
+    def _decode_rows(self, dec, cu, indptr, kvl, last, indices, indices_dev) -> _DecodeRows:
         """The decode-kernel batch of a mixed batch's one-token sequences
         ``dec``: their own CSR over a gathered copy of their page ids."""
         npg = indptr[dec + 1] - indptr[dec]
@@ -545,8 +579,8 @@ class MI355XBackend:
         i32 = lambda a: np.ascontiguousarray(a, dtype=np.int32)  # noqa: E731
         d = _DecodeRows()
         d.n = int(dec.shape[0])
-        plan, d.n_work, d.n_slots = self._plan_decode(i32(sub_ptr), i32(kvl[dec]),
-                                                      i32(last[dec]), d.n)
+        plan, d.n_work, d.n_slots, d.stride = self._plan_decode(
+            i32(sub_ptr), i32(indices[page_ix]), i32(kvl[dec]), i32(last[dec]), d.n)
         d.plan = self._upload(plan)
         d.rows = self._upload(cu[dec].astype(np.int64))
         d.indptr = self._upload(i32(sub_ptr))

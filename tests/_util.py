@@ -103,3 +103,64 @@ def assert_attention_close(got: torch.Tensor, want: torch.Tensor, atol=2e-3, rto
 
 def to_np(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().numpy()
+
+
+# ---------------------------------------------------------------- decode plan
+
+def plan_decode(kv_lens, part_pages, workgroups=512, n_kv_heads=8, ps=16, indices=None,
+                num_blocks=None):
+    """Run the library's host decode planner over sequences of ``kv_lens``
+    (page ids default to 0, 1, 2, ... in order) and parse the plan into
+    ``(indptr, bins, n_work, n_slots)``: ``bins`` a list of items in stream
+    order, each a dict of its fields with ``pages``, a list of
+    (id, live rows, bad) per page."""
+    import ctypes as C
+
+    from llm_serving_layer_amd import _native
+
+    n = len(kv_lens)
+    npages = [-(-k // ps) for k in kv_lens]
+    indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
+    if indices is None:
+        indices = np.arange(int(indptr[-1]), dtype=np.int32)
+    indices = np.ascontiguousarray(indices, dtype=np.int32)
+    if num_blocks is None:
+        num_blocks = max(1, int(indptr[-1]))
+    kvl = np.array(kv_lens, np.int32)
+    last = np.array([k % ps or ps for k in kv_lens], np.int32)
+    p = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
+    nw, ns, stride, need = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int64()
+    lib = _native.load()
+    cap = 64
+    for _ in range(2):
+        buf = np.zeros(cap, np.int32)
+        rc = lib.pkv_plan_decode(p(indptr), p(indices), p(kvl), p(last), n, ps, num_blocks,
+                                 n_kv_heads, part_pages, workgroups, p(buf), cap,
+                                 C.byref(need), C.byref(nw), C.byref(ns), C.byref(stride))
+        if rc == _native.ERR_CAPACITY and need.value > cap:
+            cap = int(need.value)
+            continue
+        break
+    _native.check(rc, "plan (decode)")
+    S = stride.value
+    heads_per_wg = 4 if n_kv_heads % 4 == 0 else 2 if n_kv_heads % 2 == 0 else 1
+    n_bins = nw.value // (n_kv_heads // heads_per_wg)
+    assert need.value == n_bins * S + 64 and not buf[n_bins * S:need.value].any()
+    bins = []
+    for b in range(n_bins):
+        blk = buf[b * S:(b + 1) * S]
+        n_items, n_pg = int(blk[0]), int(blk[1])
+        words = blk[4:4 + n_pg].astype(np.int64) & 0xFFFFFFFF
+        base = 4 + ((n_pg + 3) & ~3)
+        items, pos = [], 0
+        for i in range(n_items):
+            seq, np_, tok0, kv, slot, nparts, slot0, flags = (int(x) for x in
+                                                              blk[base + 8 * i:base + 8 * i + 8])
+            pages = [(int(w & ((1 << 27) - 1)), int((w >> 27) & 15) + 1, bool(w >> 31))
+                     for w in words[pos:pos + np_]]
+            pos += np_
+            items.append(dict(seq=seq, np=np_, tok0=tok0, kv=kv, slot=slot, nparts=nparts,
+                              slot0=slot0, last=bool(flags & 1), pages=pages))
+        assert pos == n_pg
+        bins.append(items)
+    return indptr, bins, nw.value, ns.value

@@ -20,7 +20,7 @@ from hypothesis import strategies as st
 from llm_serving_layer_amd import (BlockAllocator, ScheduledSeq, SequenceBlocks, _native,
                                    build_batch_meta)
 
-from ._util import make_meta
+from ._util import make_meta, plan_decode
 
 SETTINGS = settings(max_examples=60, deadline=None,
                     suppress_health_check=[HealthCheck.too_slow])
@@ -73,40 +73,23 @@ def test_array_assembly_equals_per_sequence_assembly(batch):
 
 
 @SETTINGS
-@given(st.lists(st.integers(1, 3000), min_size=1, max_size=200), st.integers(1, 64))
-def test_decode_plan_covers_every_page_exactly_once(kv_lens, part_pages):
-    ps = 16
-    n = len(kv_lens)
-    npages = [-(-k // ps) for k in kv_lens]
-    indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
-    kvl = np.array(kv_lens, np.int32)
-    last = np.array([k % ps or ps for k in kv_lens], np.int32)
-    cap = 8 * (int(indptr[-1]) + n)
-    buf = np.empty(cap, np.int32)
-    nw, ns = C.c_int32(), C.c_int32()
-    p = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
-    rc = _native.load().pkv_plan_decode(p(indptr), p(kvl), p(last), n, ps, part_pages,
-                                        p(buf), cap, C.byref(nw), C.byref(ns))
-    _native.check(rc, "plan")
-    work = buf[:8 * nw.value].reshape(-1, 8)
+@given(st.lists(st.integers(1, 3000), min_size=1, max_size=200), st.integers(1, 64),
+       st.integers(1, 1024))
+def test_decode_plan_covers_every_page_exactly_once(kv_lens, part_pages, workgroups):
+    indptr, bins, n_work, n_slots = plan_decode(kv_lens, part_pages, workgroups)
     covered = np.zeros(int(indptr[-1]), np.int32)
-    if ns.value == 0:   # packs of whole consecutive sequences
-        assert max(npages) <= part_pages
-        for seq0, pbase, pages, slot, nseq, tok0, nparts, slot0 in work:
-            assert pbase == indptr[seq0] and pages == indptr[seq0 + nseq] - pbase
-            assert 1 <= nseq <= 16 and pages <= part_pages
-            covered[pbase:pbase + pages] += 1
-    else:
-        assert max(npages) > part_pages
-        slots = []
-        for seq, pbase, pages, slot, kv, tok0, nparts, slot0 in work:
-            first = pbase - indptr[seq]
-            assert 1 <= pages <= part_pages and kv == kv_lens[seq] and tok0 == first * ps
-            covered[pbase:pbase + pages] += 1
-            if nparts > 1:
-                slots.append(slot)
+    slots = []
+    for items in bins:
+        for it in items:
+            seq, first = it["seq"], it["tok0"] // 16
+            assert 1 <= it["np"] <= part_pages and it["kv"] == kv_lens[seq]
+            ids = [pid for pid, _, _ in it["pages"]]
+            assert ids == list(range(indptr[seq] + first, indptr[seq] + first + it["np"]))
+            covered[indptr[seq] + first:indptr[seq] + first + it["np"]] += 1
+            if it["nparts"] > 1:
+                slots.append(it["slot"])
             else:
-                assert slot == -1
-        assert sorted(slots) == list(range(ns.value))
+                assert it["slot"] == -1
+    assert sorted(slots) == list(range(n_slots))
     assert (covered == 1).all()
-    assert list(work[:, 2]) == sorted(work[:, 2], reverse=True)
+    assert 1 <= n_work <= max(workgroups, 2)

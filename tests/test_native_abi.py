@@ -19,6 +19,8 @@ import torch
 from llm_serving_layer_amd import _native
 from llm_serving_layer_amd.backend import MI355XBackend
 
+from ._util import plan_decode
+
 HEADER = Path(__file__).resolve().parents[1] / "include" / "pagedkv.h"
 
 
@@ -40,99 +42,129 @@ def test_library_exports_every_declared_symbol():
     assert lib.pkv_abi_version() == _native.ABI_VERSION
 
 
-def plan_decode(kv_lens, part_pages, ps=16):
-    n = len(kv_lens)
-    npages = [-(-k // ps) for k in kv_lens]
-    indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
-    kvl = np.array(kv_lens, np.int32)
-    last = np.array([k % ps or ps for k in kv_lens], np.int32)
-    cap = 8 * (int(indptr[-1]) + n)
-    buf = np.empty(cap, np.int32)
-    nw, ns = C.c_int32(), C.c_int32()
-    rc = _native.load().pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), n, ps, part_pages,
-                                        ptr(buf), cap, C.byref(nw), C.byref(ns))
-    _native.check(rc, "plan")
-    return indptr, npages, buf[:8 * nw.value].reshape(-1, 8), ns.value
+def _role(it):
+    """0: a cut sequence's piece before its last, 1: a whole sequence,
+    2: a cut sequence's last piece (it merges)."""
+    return 1 if it["slot"] < 0 else 2 if it["last"] else 0
 
 
-@pytest.mark.parametrize("part_pages", [1, 3, 8, 16, 64])
-def test_decode_plan_covers_every_page_once(part_pages):
-    """Every page of every sequence is in exactly one partition."""
-    rng = random.Random(part_pages)
+@pytest.mark.parametrize("part_pages", [1, 3, 8, 10, 16, 64])
+@pytest.mark.parametrize("workgroups", [1, 96, 512])
+def test_decode_plan_covers_every_page_once(part_pages, workgroups):
+    """Every page of every sequence is in exactly one piece of one bin, with
+    its id and live row count; pieces of a sequence are consecutive and
+    nearly equal (sizes differ by at most one page); in a bin, pieces of cut
+    sequences before their last come first and last pieces last; the partial
+    slots of cut sequences are dense and unique, so no two pieces share one,
+    and every (sequence, head) arrival counter index stays below
+    n_seqs * n_kv_heads."""
+    rng = random.Random(part_pages * 1000 + workgroups)
     kv_lens = [rng.randint(1, 2048) for _ in range(300)] + [16, 64, 65, 1]
-    indptr, npages, work, n_slots = plan_decode(kv_lens, part_pages)
-    covered = [[0] * p for p in npages]
+    ids = np.array(rng.sample(range(100000), sum(-(-k // 16) for k in kv_lens)), np.int32)
+    indptr, bins, n_work, n_slots = plan_decode(kv_lens, part_pages, workgroups,
+                                                indices=ids, num_blocks=100000)
+    n_items = sum(len(b) for b in bins)
+    assert n_work == 2 * len(bins) and len(bins) == min(max(workgroups // 2, 1), n_items)
+    npages = np.diff(indptr)
+    covered = [np.zeros(k, int) for k in npages]
+    by_seq = {}
     slots = []
-    for seq, pbase, n, slot, kv, tok0, nparts, slot0 in work:
-        first = pbase - indptr[seq]
-        assert 1 <= n <= part_pages and kv == kv_lens[seq] and tok0 == first * 16
-        assert nparts == -(-npages[seq] // part_pages) and first + n <= npages[seq]
-        for p in range(first, first + n):
-            covered[seq][p] += 1
-        if nparts == 1:
-            assert slot == -1 and slot0 == -1
-        else:
-            assert slot - slot0 == first // part_pages
-            slots.append(slot)
-    assert all(all(c == 1 for c in row) for row in covered)
+    for items in bins:
+        roles = [_role(it) for it in items]
+        assert roles == sorted(roles), "cut pieces first, whole sequences, last pieces at the end"
+        for it in items:
+            seq, first = it["seq"], it["tok0"] // 16
+            assert 0 <= seq < len(kv_lens) and it["kv"] == kv_lens[seq] and it["tok0"] % 16 == 0
+            k = -(-npages[seq] // part_pages)
+            assert it["nparts"] == k and 1 <= it["np"] <= part_pages
+            assert it["last"] == (first + it["np"] == npages[seq])
+            for t, (pid, live, bad) in enumerate(it["pages"]):
+                pg = first + t
+                assert not bad and pid == ids[indptr[seq] + pg]
+                assert live == (kv_lens[seq] - 16 * pg if pg == npages[seq] - 1 else 16)
+                covered[seq][pg] += 1
+            by_seq.setdefault(seq, []).append((first, it["np"], it["slot"], it["slot0"]))
+            if k == 1:
+                assert it["slot"] == -1 and it["slot0"] == -1
+            else:
+                slots.append(it["slot"])
+    assert all((c == 1).all() for c in covered)
     assert sorted(slots) == list(range(n_slots)), "partial slots must be dense and unique"
-    assert list(work[:, 2]) == sorted(work[:, 2], reverse=True), "longest partitions first"
+    for seq, ps_ in by_seq.items():
+        ps_.sort()
+        sz = [n for _, n, _, _ in ps_]
+        assert max(sz) - min(sz) <= 1, "pieces of a sequence are nearly equal"
+        if len(ps_) > 1:  # slot = first slot + piece index, in page order
+            assert [s - s0 for _, _, s, s0 in ps_] == list(range(len(ps_)))
 
 
-@pytest.mark.parametrize("part_pages", [1, 4, 10, 64])
-def test_decode_plan_packs_consecutive_sequences_when_none_is_split(part_pages):
-    """No sequence longer than a partition: the plan has no partial slots and
-    each entry is a maximal run of consecutive whole sequences (at most 16,
-    at most part_pages pages unless a single sequence), longest first."""
-    rng = random.Random(part_pages)
-    kv_lens = [rng.randint(1, 16 * part_pages) for _ in range(500)] + [16 * part_pages, 1]
-    indptr, npages, work, n_slots = plan_decode(kv_lens, part_pages)
-    assert n_slots == 0
-    seen = []
-    for seq0, pbase, pages, slot, nseq, tok0, nparts, slot0 in work:
-        assert (slot, tok0, nparts, slot0) == (-1, 0, 1, -1)
-        assert 1 <= nseq <= 16 and pbase == indptr[seq0]
-        assert pages == indptr[seq0 + nseq] - indptr[seq0]
-        assert pages <= part_pages
-        nxt = seq0 + nseq
-        if nxt < len(kv_lens) and nseq < 16:
-            assert pages + npages[nxt] > part_pages, "pack could have taken the next sequence"
-        seen.extend(range(seq0, nxt))
-    assert sorted(seen) == list(range(len(kv_lens))), "every sequence in exactly one pack"
-    assert list(work[:, 2]) == sorted(work[:, 2], reverse=True), "longest packs first"
+@pytest.mark.parametrize("workgroups", [64, 512, 1024])
+def test_decode_plan_balances_the_bins(workgroups):
+    """LPT over the pieces' costs (pages, plus a merge for a cut sequence's
+    last piece): no bin's cost exceeds the average by more than one piece."""
+    rng = random.Random(workgroups)
+    kv_lens = [max(1, min(2048, int(round(rng.lognormvariate(5.23, 0.8))))) for _ in range(256)]
+    _, bins, _, _ = plan_decode(kv_lens, 10, workgroups)
+
+    def cost(it):
+        return 16 * it["np"] + 4 + (40 if _role(it) == 2 else 0)
+
+    loads = [sum(cost(it) for it in items) for items in bins]
+    assert max(loads) <= sum(loads) / len(loads) + 16 * 10 + 44
 
 
-def test_decode_plan_rejects_partitions_beyond_one_wave():
+def test_decode_plan_cut_depends_only_on_the_sequence():
+    """Batch invariance of the cut: a sequence's pieces (first page, size,
+    piece index) are the same alone and inside any batch."""
+    rng = random.Random(7)
+    kv_lens = [rng.randint(1, 2048) for _ in range(64)]
+
+    def cut_of(lens, seq):
+        _, bins, _, _ = plan_decode(lens, 10, 96)
+        return sorted((it["tok0"], it["np"], it["slot"] - it["slot0"] if it["slot"] >= 0 else -1)
+                      for items in bins for it in items if it["seq"] == seq)
+
+    for i in (0, 5, 63):
+        assert cut_of(kv_lens, i) == cut_of([kv_lens[i]], 0)
+
+
+def test_decode_plan_flags_out_of_range_pages():
+    """An out-of-range kv_indices entry becomes page 0 with the bad bit set
+    (the kernel reports it and never dereferences it)."""
+    ids = np.array([3, -1, 7, 50], np.int32)
+    _, bins, _, _ = plan_decode([64], 64, 2, indices=ids, num_blocks=10)
+    pages = bins[0][0]["pages"]
+    assert [(p, b) for p, _, b in pages] == [(3, False), (0, True), (7, False), (0, True)]
+
+
+def test_decode_plan_rejections():
     lib = _native.load()
     indptr = np.array([0, 1], np.int32)
-    kvl, last = np.array([16], np.int32), np.array([16], np.int32)
-    out = np.empty(16, np.int32)
-    nw, ns = C.c_int32(), C.c_int32()
+    ids = np.array([0], np.int32)
+    out = np.empty(256, np.int32)
+    nw, ns, st, need = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int64()
+
+    def plan(kvl, last, part_pages=4, num_blocks=16, cap=256):
+        rc = lib.pkv_plan_decode(ptr(indptr), ptr(ids), ptr(np.array([kvl], np.int32)),
+                                 ptr(np.array([last], np.int32)), 1, 16, num_blocks, 8,
+                                 part_pages, 512, ptr(out), cap, C.byref(need), C.byref(nw),
+                                 C.byref(ns), C.byref(st))
+        return rc
+
     for bad in (0, 65):
-        rc = lib.pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), 1, 16, bad, ptr(out), 16,
-                                 C.byref(nw), C.byref(ns))
         with pytest.raises(ValueError, match="part_pages"):
-            _native.check(rc, "plan")
+            _native.check(plan(16, 16, part_pages=bad), "plan")
+    with pytest.raises(ValueError, match="kv_last_page_len"):
+        _native.check(plan(16, 9), "plan")
+    with pytest.raises(ValueError, match="pages supplied"):
+        _native.check(plan(999, 9), "plan")
+    with pytest.raises(ValueError, match="num_blocks"):
+        _native.check(plan(16, 16, num_blocks=(1 << 27) + 1), "plan")
+    rc = plan(16, 16, cap=8)
+    assert rc == _native.ERR_CAPACITY and need.value > 8
+    assert plan(16, 16, cap=int(need.value)) == _native.OK
     assert lib.pkv_decode_fast_path(32, 8, 64, 16, _native.DTYPE_F16, 64) == 1
     assert lib.pkv_decode_fast_path(32, 8, 64, 16, _native.DTYPE_F16, 65) == 0
-
-
-def test_decode_plan_rejects_inconsistent_metadata():
-    lib = _native.load()
-    indptr = np.array([0, 1], np.int32)
-    out = np.empty(16, np.int32)
-    nw, ns = C.c_int32(), C.c_int32()
-    kvl = np.array([16], np.int32)
-    last = np.array([9], np.int32)
-    rc = lib.pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), 1, 16, 4, ptr(out), 16,
-                             C.byref(nw), C.byref(ns))
-    with pytest.raises(ValueError, match="kv_last_page_len"):
-        _native.check(rc, "plan")
-    kvl[0] = 999
-    rc = lib.pkv_plan_decode(ptr(indptr), ptr(kvl), ptr(last), 1, 16, 4, ptr(out), 16,
-                             C.byref(nw), C.byref(ns))
-    with pytest.raises(ValueError, match="pages supplied"):
-        _native.check(rc, "plan")
 
 
 def test_prefill_plan_covers_every_query_row_once():
@@ -193,6 +225,8 @@ def _host_backend(part_pages=10):
     bk.part_pages = part_pages
     bk.q_tile = bk._prefill_tile = bk._lib.pkv_prefill_q_tile(32, 8, 64, 16, _native.DTYPE_F16)
     bk._split_mixed = True
+    bk._fast_decode = True
+    bk._decode_wgs = 512     # what pkv_decode_workgroups gives on a 256-CU device
     bk._upload = lambda a: torch.from_numpy(np.array(a))   # CPU tensors stand in
     bk._workspace = torch.zeros(0, dtype=torch.uint8)
     bk._planned, bk._slot_cache, bk._pending = None, None, None
@@ -215,7 +249,9 @@ def test_backend_plans_decode_and_prefill_through_the_library():
     dec = grow_and_assemble(seqs, [1, 1, 1], 16)
     p = bk._ensure_planned(dec)
     assert not p.use_prefill and p.fusable and p.n_slots > 0
-    assert p.plan.numel() == 8 * p.n_work
+    bins = p.n_work // 2
+    assert p.plan.numel() == bins * p.stride + 64
+    assert sum(int(p.plan[b * p.stride + 1]) for b in range(bins)) == 3 + 7 + 1, "every page"
     assert bk._workspace.numel() >= bk._lib.pkv_decode_workspace_bytes(
         3, p.n_slots, 32, 8, 64)
 
@@ -243,5 +279,9 @@ def test_mixed_batch_plans_its_decodes_for_the_decode_kernel():
     indptr, indices = meta.kv_indptr.tolist(), meta.kv_indices.tolist()
     want = indices[indptr[0]:indptr[1]] + indices[indptr[2]:indptr[3]]
     assert d.indices.tolist() == want and d.indptr.tolist() == [0, 3, 4]
-    work = d.plan.reshape(-1, 8).numpy()
-    assert d.n_slots > 0 and set(work[:, 0]) == {0, 1}, "decode plan over the sub-batch"
+    seqs_planned = set()
+    for b in range(d.n_work // 2):
+        blk = d.plan[b * d.stride:(b + 1) * d.stride].numpy()
+        base = 4 + ((int(blk[1]) + 3) & ~3)
+        seqs_planned |= {int(blk[base + 8 * i]) for i in range(int(blk[0]))}
+    assert d.n_slots > 0 and seqs_planned == {0, 1}, "decode plan over the sub-batch"

@@ -15,6 +15,8 @@ import numpy as np
 import pytest
 
 from llm_serving_layer_amd import _native
+
+from ._util import plan_decode
 from llm_serving_layer_amd.sizing import (LLAMA_3_2_1B, MI355X_HBM_BYTES, SizingError,
                                           block_bytes, decode_workspace_bound,
                                           decode_workspace_slots, kv_bytes_per_token,
@@ -108,19 +110,9 @@ def test_plan_self_consistent_across_configurations(block_size, headroom_gib, ma
 
 
 def _plan_slots(kv_lens, part_pages, ps=16):
-    """n_slots of the library's decode plan for these lengths."""
-    npages = [-(-k // ps) for k in kv_lens]
-    indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
-    kvl = np.array(kv_lens, np.int32)
-    last = np.array([k % ps or ps for k in kv_lens], np.int32)
-    cap = 8 * (int(indptr[-1]) + len(kv_lens))
-    buf = np.empty(cap, np.int32)
-    nw, ns = C.c_int32(), C.c_int32()
-    p = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
-    rc = _native.load().pkv_plan_decode(p(indptr), p(kvl), p(last), len(kv_lens), ps,
-                                        part_pages, p(buf), cap, C.byref(nw), C.byref(ns))
-    _native.check(rc, "plan")
-    return int(indptr[-1]), ns.value
+    """(pages, n_slots) of the library's decode plan for these lengths."""
+    indptr, _, _, n_slots = plan_decode(kv_lens, part_pages, 512, ps=ps)
+    return int(indptr[-1]), n_slots
 
 
 @pytest.mark.parametrize("part_pages", [1, 3, 10, 64])

@@ -50,7 +50,7 @@ def _call(lib, fn_name, bk, p, q, out, k, v, with_workspace):
     args = [q.data_ptr(), out.data_ptr(), bk._k_pool[0].data_ptr(), bk._v_pool[0].data_ptr(),
             bk.num_blocks, p.indptr.data_ptr(), p.indices.data_ptr(), p.kv_lens.data_ptr(),
             p.n_seqs, 32, 8, 64, 16, 0.125, _native.DTYPE_F16, p.plan.data_ptr(), p.n_work,
-            p.n_slots, bk.part_pages, k.data_ptr() if k is not None else None,
+            p.n_slots, p.stride, k.data_ptr() if k is not None else None,
             v.data_ptr() if v is not None else None,
             p.slots.data_ptr() if k is not None else None]
     if with_workspace:
@@ -98,7 +98,7 @@ def test_noalloc_rejects_a_plan_beyond_its_array():
     rc = lib.pkv_attend_decode_noalloc(
         dummy.data_ptr(), dummy.data_ptr(), dummy.data_ptr(), dummy.data_ptr(), 1,
         dummy.data_ptr(), dummy.data_ptr(), dummy.data_ptr(), 1, 32, 8, 64, 16, 0.125,
-        _native.DTYPE_F16, dummy.data_ptr(), 1, n_slots, 10, None, None, None,
+        _native.DTYPE_F16, dummy.data_ptr(), 2, n_slots, 4, None, None, None,
         dummy.data_ptr(), _current_stream(torch.device(DEV)))
     assert rc == _native.ERR_CAPACITY
     assert b"at most" in lib.pkv_last_error()
