@@ -52,7 +52,7 @@ __all__ = ["MI355XBackend", "is_available", "unavailable_reason"]
 _DTYPES = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16,
            torch.float32: _native.DTYPE_F32}
 
-DEFAULT_PART_PAGES = 10  # split-K partition: 10 pages = 160 tokens
+DEFAULT_PART_PAGES = 20  # split-K partition: 20 pages = 320 tokens
 MAX_PART_PAGES = 64      # a partition's page ids are read by one wavefront
 DEFAULT_Q_TILE = 64      # prefill tile when the geometry has no matrix-core kernel
 
