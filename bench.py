@@ -31,6 +31,11 @@ Other workloads (one JSON line each, same fields):
   capacity  decode at 4096 sequences of 16..64 tokens, then 512 sequences of
             lognormal mean 2048 (clipped to 2048), pool of ~200 GB; GB/s.
   calib     a 1 GiB device copy, the known-size reference for HBM counters.
+  timeline  the headline decode launch under the instrumented build
+            (``python -m llm_serving_layer_amd.build --timeline``, loaded with
+            PKV_LIBRARY=llm_serving_layer_amd/_native/libpagedkv_timeline.so):
+            per-wave start / first page / last page / end times, summarised
+            as ramp, steady stream and tail. Not a throughput line.
 """
 
 from __future__ import annotations
@@ -434,6 +439,94 @@ def cpu_baseline(lens, budget_s=10.0):
                               "sample": f"{n1} passes, median {one_s * 1e3:.1f} ms/layer"}}
 
 
+# ---------------------------------------------------------------- timeline ---
+
+def bench_timeline(args):
+    """
+    Ramp / steady / tail of one headline decode launch, from the per-wave
+    records of the instrumented build (100 MHz s_memrealtime ticks): each wave
+    (one KV head of one bin) records its start, the end of its first and last
+    page, its end (after any merge), its page and item counts, and its merges
+    with the time they took. Every layer's launch runs the same plan, so the
+    records the last launch leaves describe the launch.
+    """
+    import ctypes as C
+    import torch
+    from llm_serving_layer_amd import _native
+
+    lib = _native.load()
+    if not hasattr(lib, "pkv_timeline_read"):
+        raise RuntimeError("the timeline workload needs the instrumented build: run "
+                           "`python -m llm_serving_layer_amd.build --timeline` and set "
+                           "PKV_LIBRARY=llm_serving_layer_amd/_native/libpagedkv_timeline.so")
+    lib.pkv_timeline_read.restype = C.c_int
+    lib.pkv_timeline_read.argtypes = [C.c_void_p, C.c_int64]
+    lens = lognormal_lengths(256, 256)
+    pages = sum(-(-n // BS) for n in lens)
+    bk, meta, step, _, ctx = decode_setup("cuda:0", lens, 2 * pages, args.part_pages)
+    log("graph replay (instrumented build)")
+    graph, _g = time_graph(step, args.steps, args.warmup)
+    bk.check_device_errors()
+    buf = np.zeros(16384 * 8, dtype=np.uint64)
+    if lib.pkv_timeline_read(buf.ctypes.data, buf.nbytes) != 0:
+        raise RuntimeError("pkv_timeline_read failed")
+    t = buf.reshape(-1, 8).astype(np.int64)
+    wid = np.nonzero(t[:, 0] > 0)[0]   # waves of bins with no item record nothing
+    t = t[wid]
+    t0 = t[:, 0].min()
+    start, first, last, end = [(t[:, i] - t0) / 100.0 for i in range(4)]
+    npg, nit, nmg = t[:, 4], t[:, 5], t[:, 6]
+    merge_us = t[:, 7] / 100.0
+
+    def pct(v):
+        return {k: round(float(np.percentile(v, q)), 2)
+                for k, q in (("p10", 10), ("p50", 50), ("p90", 90), ("max", 100))}
+
+    page_bytes = 2 * BS * D * 2       # one KV head's K and V slice of a page
+    rate = (npg - 1) / np.maximum(last - first, 1e-3)   # pages per us, per wave
+    span = float(end.max())
+    layer_bytes = decode_bytes(lens, pages)
+    # waves still running, every half microsecond of the launch
+    grid = np.arange(0.0, span + 0.5, 0.5)
+    active = [int(((start <= x) & (end > x)).sum()) for x in grid]
+    line = base_line(
+        args, "decode launch timeline (per-wave, instrumented build)", round(span, 2), "us",
+        graph["ms_per_step"], "fp16",
+        ("one paged decode launch of the batch-256 headline step (lognormal mean 258), "
+         f"{GEOM}"),
+        batch=256, pages=pages, part_pages=args.part_pages)
+    # wave w of the grid: workgroup w // waves (dispatched round-robin over
+    # the 8 XCDs), KV head group (workgroup % groups), head in the group w % waves
+    hgw = 4 if HKV % 4 == 0 else 2 if HKV % 2 == 0 else 1
+    head = (wid // hgw % (HKV // hgw)) * hgw + wid % hgw
+    xcd = (wid // hgw) % 8
+
+    def by(key, n):
+        return [{"pages_per_us_p50": round(float(np.median(rate[key == i])), 3),
+                 "last_page_done_p90": round(float(np.percentile(last[key == i], 90)), 2)}
+                for i in range(n)]
+
+    line.update({
+        "higher_is_better": False,
+        "launch_us_graph_replay": round(graph["ms_per_step"] * 1e3 / LAYERS, 2),
+        "by_kv_head": by(head, HKV), "by_xcd": by(xcd, 8),
+        "waves": int(len(t)),
+        "ramp_us": {"start": pct(start), "first_page_done": pct(first)},
+        "steady": {"pages_per_wave": pct(npg), "items_per_wave": pct(nit),
+                   "pages_per_us_per_wave": pct(rate),
+                   "stream_GBps_all_waves": round(float(rate.sum()) * page_bytes / 1e3, 1),
+                   "page_bytes_per_wave": page_bytes},
+        "tail_us": {"last_page_done": pct(last), "end": pct(end),
+                    "end_minus_last_page": pct(end - last)},
+        "merges": {"count": int(nmg.sum()), "waves_merging": int((nmg > 0).sum()),
+                   "us_per_merge": round(float(merge_us.sum() / max(int(nmg.sum()), 1)), 2)},
+        "span_us": round(span, 2),
+        "span_GBps": round(layer_bytes / (span * 1e-6) / 1e9, 1),
+        "active_waves_every_0p5us": active,
+    })
+    return line
+
+
 # ---------------------------------------------------------------- capacity ---
 
 def bench_capacity(args):
@@ -726,7 +819,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "prefill", "copy", "swap", "capacity", "calib"])
+                    choices=["decode", "prefill", "copy", "swap", "capacity", "calib",
+                             "timeline"])
     ap.add_argument("--part-pages", type=int, default=None,
                     help="split-K partition size in pages (default: the backend's)")
     ap.add_argument("--eager", action="store_true",
@@ -743,7 +837,8 @@ def main() -> int:
         from llm_serving_layer_amd.backend import DEFAULT_PART_PAGES
         args.part_pages = DEFAULT_PART_PAGES
     fn = {"decode": bench_decode, "prefill": bench_prefill, "copy": bench_copy,
-          "swap": bench_swap, "capacity": bench_capacity, "calib": bench_calib}[args.workload]
+          "swap": bench_swap, "capacity": bench_capacity, "calib": bench_calib,
+          "timeline": bench_timeline}[args.workload]
     print(json.dumps(fn(args)))
     return 0
 

@@ -195,6 +195,19 @@ __device__ __forceinline__ void merge_head(T* __restrict__ out, float* wts, int 
   }
 }
 
+#ifdef PKV_TIMELINE
+// Instrumented build only (-DPKV_TIMELINE): every wave records, in 100 MHz
+// s_memrealtime ticks, {start, first page done, last page done, end,
+// pages, items, merges, ticks spent merging} with plain vector stores, for
+// wave blockIdx.x * waves + wave below kTimelineWaves. Read back with
+// pkv_timeline_read.
+constexpr int kTimelineWaves = 16384;
+__device__ unsigned long long pkv_timeline[kTimelineWaves * 8];
+#define PKV_TL(...) __VA_ARGS__
+#else
+#define PKV_TL(...)
+#endif
+
 // One wave's LDS tile: 16 K rows then 16 V rows of its head, each padded by
 // 16 bytes so the K operand reads and the transposed V reads of a wave spread
 // over the banks.
@@ -247,6 +260,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   static_assert(OPS * (kDepth - 1) < 64, "vmcnt field");
 
   extern __shared__ __align__(16) unsigned char smem[];
+  PKV_TL(const unsigned long long tl_start = __builtin_amdgcn_s_memrealtime();
+         unsigned long long tl_first = 0, tl_merge = 0; int tl_merges = 0;)
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int hgw = blockDim.x >> 6;                   // KV heads of this workgroup
@@ -391,11 +406,13 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
 
   // Merge (seq, h) from the stored partials and reset its counter.
   auto merge = [&](int sq, int nparts, int slot0) {
+    PKV_TL(const unsigned long long tm = __builtin_amdgcn_s_memrealtime(); ++tl_merges;)
     merge_head<T, D, G>(out, reinterpret_cast<float*>(kl), sq, h, n_kv_heads, nparts, slot0,
                         ro, rm);
     if (lane == 0)
       __hip_atomic_store(counters + (int64_t)sq * n_kv_heads + h, 0, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
+    PKV_TL(tl_merge += __builtin_amdgcn_s_memrealtime() - tm;)
   };
   // Count an arrival whose partial has completed; the returned count.
   auto arrive = [&](int sq) -> int {
@@ -580,6 +597,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
           load_page(pn, kr[s], vr[s]);
         }
         compute(p);
+        PKV_TL(if (p == 0) tl_first = __builtin_amdgcn_s_memrealtime();)
         // (after compute: a merge below uses the wave's tile as scratch)
         if (pa_state != 0 && p == pa_at) {
           if (pa_state == 1) {
@@ -599,7 +617,23 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       }
     }
   }
+  PKV_TL(const unsigned long long tl_last = __builtin_amdgcn_s_memrealtime();)
   flush_arrival();
+#ifdef PKV_TIMELINE
+  {
+    const int wid = blockIdx.x * hgw + wave;
+    const unsigned long long tl_end = __builtin_amdgcn_s_memrealtime();
+    if (lane < 8 && wid < kTimelineWaves) {
+      const unsigned long long rec[8] = {tl_start, tl_first, tl_last, tl_end,
+                                         (unsigned long long)n_pages, (unsigned long long)n_items,
+                                         (unsigned long long)tl_merges, tl_merge};
+      unsigned long long v = rec[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) v = lane == i ? rec[i] : v;
+      pkv_timeline[(int64_t)wid * 8 + lane] = v;
+    }
+  }
+#endif
 }
 
 static size_t decode_lds_bytes(int hgw, int D) {
@@ -985,3 +1019,13 @@ extern "C" int pkv_attend_decode_noalloc(const void* q, void* out, void* k_pool,
                        n_work, n_slots, plan_stride, k_new, v_new, slot_mapping, ws,
                        (int64_t)PKV_DECODE_SCRATCH_BYTES, true, status_word, stream);
 }
+
+#ifdef PKV_TIMELINE
+// Copies the instrumented build's per-wave decode timeline (the last launch
+// that wrote each record) to host memory: at most `bytes` bytes.
+extern "C" int pkv_timeline_read(void* host, int64_t bytes) {
+  if (bytes > (int64_t)sizeof(pkv::pkv_timeline)) bytes = sizeof(pkv::pkv_timeline);
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(pkv::pkv_timeline), (size_t)bytes, 0,
+                             hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+#endif
