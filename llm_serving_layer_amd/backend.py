@@ -46,13 +46,13 @@ import torch
 
 from . import _native
 from .contract import BatchMeta
+from .sizing import DEFAULT_PART_PAGES  # split-K partition: 20 pages = 320 tokens
 
 __all__ = ["MI355XBackend", "is_available", "unavailable_reason"]
 
 _DTYPES = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16,
            torch.float32: _native.DTYPE_F32}
 
-DEFAULT_PART_PAGES = 20  # split-K partition: 20 pages = 320 tokens
 MAX_PART_PAGES = 64      # a partition's page ids are read by one wavefront
 DEFAULT_Q_TILE = 64      # prefill tile when the geometry has no matrix-core kernel
 

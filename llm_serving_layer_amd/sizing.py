@@ -51,6 +51,9 @@ DEFAULT_BLOCK_SIZE = 16
 #: Largest batch the decode workspace is reserved for by default: the
 #: 4096-sequence capacity workload.
 DEFAULT_MAX_BATCH_SEQS = 4096
+# Split-K partition of the decode kernel, in pages (320 tokens): the
+# backend's default, so the workspace reserved here is the one it uses.
+DEFAULT_PART_PAGES = 20
 #: Longest sequence the decode workspace is reserved for by default (the
 #: reference's max_seq, bench/capacity.py:196-242).
 DEFAULT_MAX_SEQ_LEN = 2048
@@ -299,7 +302,8 @@ def plan_kv_pool(total_vram_bytes: int | None = MI355X_HBM_BYTES,
                  activation_headroom_bytes: int = DEFAULT_ACTIVATION_HEADROOM_BYTES,
                  block_size: int = DEFAULT_BLOCK_SIZE, shape: ModelKVShape = LLAMA_3_2_1B,
                  notes: Sequence[str] | None = None, *, n_heads: int = 32,
-                 max_batch_seqs: int = DEFAULT_MAX_BATCH_SEQS, part_pages: int = 10,
+                 max_batch_seqs: int = DEFAULT_MAX_BATCH_SEQS,
+                 part_pages: int = DEFAULT_PART_PAGES,
                  max_seq_len: int = DEFAULT_MAX_SEQ_LEN, shared_blocks: bool = True,
                  device="cuda:0") -> KVPoolPlan:
     """

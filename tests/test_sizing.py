@@ -17,8 +17,8 @@ import pytest
 from llm_serving_layer_amd import _native
 
 from ._util import plan_decode
-from llm_serving_layer_amd.sizing import (LLAMA_3_2_1B, MI355X_HBM_BYTES, SizingError,
-                                          block_bytes, decode_workspace_bound,
+from llm_serving_layer_amd.sizing import (DEFAULT_PART_PAGES, LLAMA_3_2_1B, MI355X_HBM_BYTES,
+                                          SizingError, block_bytes, decode_workspace_bound,
                                           decode_workspace_slots, kv_bytes_per_token,
                                           plan_kv_pool)
 
@@ -84,14 +84,16 @@ def test_mi355x_plan_by_hand():
     assert bare.num_blocks == 581_013
     plan = plan_kv_pool()
     assert 0 < bare.num_blocks - plan.num_blocks < 2000
-    assert plan.workspace_bytes == decode_workspace_bound(plan.num_blocks, 4096, 32, 8, 64, 10)
+    assert plan.workspace_bytes == decode_workspace_bound(plan.num_blocks, 4096, 32, 8, 64,
+                                                          DEFAULT_PART_PAGES)
     # ~200 GB capacity pool of the capacity workload fits with room to spare
     assert plan.num_blocks > 381_469
 
 
 def test_plan_is_self_consistent_one_more_block_would_not_fit():
     plan = plan_kv_pool()
-    ws_next = decode_workspace_bound(plan.num_blocks + 1, 4096, 32, 8, 64, 10)
+    ws_next = decode_workspace_bound(plan.num_blocks + 1, 4096, 32, 8, 64,
+                                     DEFAULT_PART_PAGES)
     assert plan.num_blocks * plan.bytes_per_block + plan.workspace_bytes <= plan.available_bytes
     assert (plan.num_blocks + 1) * plan.bytes_per_block + ws_next > plan.available_bytes
     assert plan.is_self_consistent()
