@@ -108,7 +108,7 @@ class MI355XBackend:
                  dtype: torch.dtype = torch.float16, *,
                  part_pages: int = DEFAULT_PART_PAGES, q_tile: int | None = None,
                  fuse_append: bool = True, decode_workgroups_per_cu: int = 2,
-                 decode_workgroups: int | None = None):
+                 decode_workgroups: int | None = None, decode_workspace_bytes: int = 0):
         if n_heads % n_kv_heads != 0:
             raise ValueError(
                 f"n_heads={n_heads} must be divisible by n_kv_heads={n_kv_heads}; "
@@ -133,6 +133,8 @@ class MI355XBackend:
                              "positive")
         if decode_workgroups is not None and decode_workgroups < 1:
             raise ValueError(f"decode_workgroups={decode_workgroups} must be positive")
+        if decode_workspace_bytes < 0:
+            raise ValueError(f"decode_workspace_bytes={decode_workspace_bytes} must be >= 0")
         try:
             self._lib = _native.load()
         except RuntimeError as exc:
@@ -188,7 +190,11 @@ class MI355XBackend:
         self._block_bytes = block_size * n_kv_heads * head_dim * self._pool.element_size()
         self._plane_bytes = num_blocks * self._block_bytes
         self._status = torch.zeros(1, dtype=torch.int32, device=self.device)
-        self._workspace = torch.zeros(0, dtype=torch.uint8, device=self.device)
+        # The split-K workspace. A pool sized by sizing.plan_kv_pool passes its
+        # workspace_bytes here, so no batch within that plan's limits ever
+        # allocates at run time; a plan that needs more grows it.
+        self._workspace = torch.zeros(decode_workspace_bytes, dtype=torch.uint8,
+                                      device=self.device)
         self._planned: _Plan | None = None
         self._slot_cache: tuple[BatchMeta, torch.Tensor] | None = None
         self._pending: _Pending | None = None
@@ -547,25 +553,35 @@ class MI355XBackend:
         n_work, n_slots, stride = C.c_int32(), C.c_int32(), C.c_int32()
         needed = C.c_int64()
         cap = 6 * self._decode_wgs + 2 * int(indptr32[-1]) + 24 * n + 128
-        for _ in range(2):
-            buf = np.empty(cap, dtype=np.int32)
-            rc = self._lib.pkv_plan_decode(
-                ptr(indptr32), ptr(indices32), ptr(kvl32), ptr(last32), n, self.block_size,
-                self.num_blocks, self.n_kv_heads, self.part_pages, self._decode_wgs, ptr(buf),
-                cap, C.byref(needed), C.byref(n_work), C.byref(n_slots), C.byref(stride))
-            if rc == _native.ERR_CAPACITY and needed.value > cap:
-                cap = int(needed.value)
-                continue
-            break
-        _native.check(rc, "plan (decode)")
-        need = self._lib.pkv_decode_workspace_bytes(n, n_slots.value, self.n_heads,
-                                                    self.n_kv_heads, self.head_dim)
+        counter_bytes = (4 * n * self.n_kv_heads + 255) // 256 * 256
+        part_pages = self.part_pages
+        while True:
+            for _ in range(2):
+                buf = np.empty(cap, dtype=np.int32)
+                rc = self._lib.pkv_plan_decode(
+                    ptr(indptr32), ptr(indices32), ptr(kvl32), ptr(last32), n,
+                    self.block_size, self.num_blocks, self.n_kv_heads, part_pages,
+                    self._decode_wgs, ptr(buf), cap, C.byref(needed), C.byref(n_work),
+                    C.byref(n_slots), C.byref(stride))
+                if rc == _native.ERR_CAPACITY and needed.value > cap:
+                    cap = int(needed.value)
+                    continue
+                break
+            _native.check(rc, "plan (decode)")
+            need = self._lib.pkv_decode_workspace_bytes(n, n_slots.value, self.n_heads,
+                                                        self.n_kv_heads, self.head_dim)
+            # The kernel addresses the partials with 32-bit buffer offsets
+            # (at most 2 GiB). A batch whose partials would not fit is cut
+            # into larger pieces for this launch only (its bits then differ
+            # from a solo run's, which is cut at part_pages).
+            if need - counter_bytes < 2**31 - 1 or part_pages >= MAX_PART_PAGES:
+                break
+            part_pages = min(2 * part_pages, MAX_PART_PAGES)
         if need > self._workspace.numel():
             # zero-filled: the arrival counters at the front start at zero
             self._workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)
         elif need > 0:
             # a previous layout may have left partial data where counters now sit
-            counter_bytes = (4 * n * self.n_kv_heads + 255) // 256 * 256
             self._workspace[:counter_bytes].zero_()
         return (buf[:int(needed.value)].copy(), n_work.value, n_slots.value, stride.value)
 

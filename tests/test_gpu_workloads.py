@@ -58,10 +58,11 @@ class _Decode:
     """A one-layer fp16 GPU backend and the fp32 oracle over the same pages,
     with each sequence's history written through both appends."""
 
-    def __init__(self, lens, seed, part_pages=DEFAULT_PART_PAGES, slack=1.25):
+    def __init__(self, lens, seed, part_pages=DEFAULT_PART_PAGES, slack=1.25, **backend_kw):
         pages = sum(-(-(n + 1) // 16) for n in lens)
         nb = int(pages * slack) + 8
-        self.gpu = MI355XBackend(1, nb, 16, 8, 32, 64, device=DEV, part_pages=part_pages)
+        self.gpu = MI355XBackend(1, nb, 16, 8, 32, 64, device=DEV, part_pages=part_pages,
+                                 **backend_kw)
         self.ref = PagedTorchOracle(1, nb, 16, 8, 32, 64, device="cpu", dtype=torch.float32)
         alloc = _shuffled(nb, seed)
         self.seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(len(lens))]
@@ -188,6 +189,24 @@ def test_headline_batch256_decode_vs_oracle(part_pages):
     d = _Decode([n - 1 for n in lens], 5, part_pages=part_pages, slack=2.0)
     d.step(f"batch 256 part_pages={part_pages}")
     d.step(f"batch 256 part_pages={part_pages}, second step")
+
+
+def test_workspace_reserved_by_the_sizing_bound_is_never_regrown():
+    """A backend given the sizing bound's workspace up front (as a pool sized
+    by plan_kv_pool is) runs the headline batch without allocating: the
+    workspace keeps its size and address, and the outputs match the oracle."""
+    from llm_serving_layer_amd.sizing import decode_workspace_bound
+
+    print("headline batch 256 on a reserved workspace", flush=True)
+    lens = lognormal_lengths(256, 256, 0.8, 2048, SEED)
+    nb = int(sum(-(-n // 16) for n in lens) * 2.0) + 8
+    reserve = decode_workspace_bound(nb, 256, 32, 8, 64, DEFAULT_PART_PAGES)
+    d = _Decode([n - 1 for n in lens], 7, slack=2.0, decode_workspace_bytes=reserve)
+    addr = d.gpu._workspace.data_ptr()
+    assert d.gpu.workspace_bytes() == reserve
+    d.step("batch 256 on the reserved workspace")
+    assert d.gpu._planned.n_slots > 0
+    assert d.gpu.workspace_bytes() == reserve and d.gpu._workspace.data_ptr() == addr
 
 
 def test_headline_step_graph_replayed_vs_oracle():

@@ -285,3 +285,29 @@ def test_mixed_batch_plans_its_decodes_for_the_decode_kernel():
         base = 4 + ((int(blk[1]) + 3) & ~3)
         seqs_planned |= {int(blk[base + 8 * i]) for i in range(int(blk[0]))}
     assert d.n_slots > 0 and seqs_planned == {0, 1}, "decode plan over the sub-batch"
+
+
+def test_decode_plan_falls_back_to_larger_pieces_past_2gib_of_partials():
+    """4096 sequences of 2048 tokens cut into 1-page pieces would need
+    524 288 partial slots (4.4 GB, past the kernel's 32-bit buffer offsets):
+    the backend re-plans that launch with pieces twice as large until the
+    partials fit (4 pages: 131 072 slots, 1.1 GB)."""
+    class _Reserved:   # a workspace already large enough: nothing is allocated
+        def numel(self):
+            return 1 << 40
+
+        def __getitem__(self, _):
+            return torch.zeros(0, dtype=torch.uint8)
+
+    bk = _host_backend(part_pages=1)
+    bk._workspace = _Reserved()
+    n, pages = 4096, 128
+    indptr = np.arange(0, (n + 1) * pages, pages, dtype=np.int32)
+    indices = np.arange(n * pages, dtype=np.int32) % 64
+    kvl = np.full(n, pages * 16, np.int32)
+    last = np.full(n, 16, np.int32)
+    plan, n_work, n_slots, stride = bk._plan_decode(indptr, indices, kvl, last, n)
+    assert n_slots == n * pages // 4
+    need = bk._lib.pkv_decode_workspace_bytes(n, n_slots, 32, 8, 64)
+    assert need < 2**31
+    assert bk._lib.pkv_decode_workspace_bytes(n, n * pages // 2, 32, 8, 64) > 2**31
