@@ -53,6 +53,28 @@ template <> struct Mma32<__bf16> {
   }
 };
 
+// LDS of one workgroup: a ring of four K/V tile buffers, each its own
+// variable (so the compiler's wait before a tile read covers only the loads
+// into that buffer), rows unpadded with 16-byte chunks XOR-swizzled by row.
+template <typename T, int D> struct PrefillLds {
+  static constexpr int TT = 32;                        // KV tokens per tile
+  static constexpr int RB = D * (int)sizeof(T);        // bytes of one head's row
+  static constexpr int TILE = TT * RB;                 // one K (or V) tile
+  static constexpr int LPT = TILE / (kPrefillThreads * 16);  // 16-byte loads per thread
+};
+
+// Row `row` of a tile stores its 16-byte chunk c at chunk position
+// c ^ xr(row), xr a permutation of row & 7. Eight consecutive rows reading
+// the same chunk (the K operand reads) then hit eight different chunk
+// positions, and so do four consecutive rows reading chunks 2j and 2j + 1
+// (the transposed V reads): both are free of bank conflicts.
+__device__ __forceinline__ int xr(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+// Byte offset of element `e` (of 2-byte elements) in row `row` of a tile.
+template <int RB>
+__device__ __forceinline__ int swz(int row, int e) {
+  return row * RB + ((((e >> 3) ^ xr(row)) & 7) | ((e >> 3) & ~7)) * 16 + (e & 7) * 2;
+}
+
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
     const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kpool,
@@ -62,21 +84,24 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
     int32_t n_kv_heads, float scale_log2, int32_t* status) {
   typedef typename Mma<T>::vec8 vec8;
   typedef typename Mma<T>::vec4 vec4;
-  constexpr int TT = 32;                 // KV tokens per tile
+  typedef PrefillLds<T, D> L;
+  constexpr int TT = L::TT;
   constexpr int PS = 16;
   constexpr int NH = TT / 32;            // 32-key halves per tile
   constexpr int NC = D / 16;             // QK k-chunks of 16 dims
   constexpr int NDH = D / 32;            // PV blocks of 32 dims
-  constexpr int NT = kPrefillThreads;
-  constexpr int RSB = D * (int)sizeof(T) + 16;
-  constexpr int CPR = D * (int)sizeof(T) / 16;
-  constexpr int CPT = TT * CPR / NT;
-  static_assert(CPT >= 1 && TT * CPR % NT == 0, "tile must split evenly over the threads");
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  auto lds_tile = [&](int buf, int kv) { return lds_raw + (buf * 2 + kv) * TT * RSB; };
+  constexpr int RB = L::RB;
+  constexpr int CPR = RB / 16;           // 16-byte chunks per row
+  constexpr int LPT = L::LPT;
+  static_assert(LPT >= 1 && L::TILE == LPT * kPrefillThreads * 16, "whole 1 KiB wave loads");
+  static_assert(64 % CPR == 0 && PS % (64 / CPR) == 0, "a wave load stays in one page");
+  __shared__ __align__(16) unsigned char buf0[2 * L::TILE];
+  __shared__ __align__(16) unsigned char buf1[2 * L::TILE];
+  __shared__ __align__(16) unsigned char buf2[2 * L::TILE];
+  __shared__ __align__(16) unsigned char buf3[2 * L::TILE];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int n = lane & 31, g = lane >> 5;
   const int item = blockIdx.x / n_kv_heads;
@@ -108,42 +133,56 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
     }
   }
 
-  // Each wave's share of a tile lies in one page (its lanes cover 64 x 16
-  // bytes of consecutive rows of a page), so the page id is a scalar read
-  // and the page a buffer range: rows at or past kv_len and tiles past the
-  // end read zeros without touching memory, and every tile issues the same
-  // loads (exact wait counts in the pipelined loop).
+  // Tiles past the end and rows at or past kv_len are outside their buffer
+  // ranges: nothing is read for them. The ring starts zeroed, so what such
+  // rows hold in LDS is finite and only ever meets zero probabilities.
+  for (int i = tid; i < 2 * L::TILE / 16; i += kPrefillThreads) {
+    reinterpret_cast<u32x4*>(buf0)[i] = u32x4{0u, 0u, 0u, 0u};
+    reinterpret_cast<u32x4*>(buf1)[i] = u32x4{0u, 0u, 0u, 0u};
+    reinterpret_cast<u32x4*>(buf2)[i] = u32x4{0u, 0u, 0u, 0u};
+    reinterpret_cast<u32x4*>(buf3)[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // Load k of a tile covers 64 x 16 bytes = 64 / CPR consecutive rows, all in
+  // one page: its page id is wave-uniform, read with a scalar load a tile
+  // ahead. (Scalar loads, so the vector-memory count holds tile loads only:
+  // a plain vector load may complete before a direct-to-LDS load issued
+  // earlier, so the count cannot prove a tile landed if the two mix.)
   const int npages = (kv_len + PS - 1) / PS;
   const uint32_t rowbytes = (uint32_t)(row * sizeof(T));
-  auto load_tile = [&](int t, vec8* kr, vec8* vr) {
+  auto page_of = [&](int t, int k) { return (t * TT + ((k * 4 + wave) * 64) / CPR) / PS; };
+  auto load_ids = [&](int t, int* ids) {   // this wave's page ids for tile t
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int c = tid + NT * k;
-      const int tk0 = t * TT + __builtin_amdgcn_readfirstlane((wave * 64 + NT * k) / CPR);
-      const int pg = tk0 / PS;
-      const int live_rows = min(PS, kv_len - pg * PS);   // <= 0 past the end
-      const int raw = kv_indices[pbase + min(pg, npages - 1)];
-      const bool bad = raw < 0 || (int64_t)raw >= num_blocks;
-      if (bad && lane == 0) flag(status, PKV_STATUS_BAD_PAGE);
-      const int pid = __builtin_amdgcn_readfirstlane(bad ? 0 : raw);
-      const __amdgpu_buffer_rsrc_t rk = ws_rsrc(const_cast<T*>(kpool) + (int64_t)pid * PS * row,
-                                                live_rows > 0 ? live_rows * rowbytes : 0);
-      const __amdgpu_buffer_rsrc_t rv = ws_rsrc(const_cast<T*>(vpool) + (int64_t)pid * PS * row,
-                                                live_rows > 0 ? live_rows * rowbytes : 0);
-      const uint32_t off = (uint32_t)(((c / CPR) % PS) * rowbytes + (h * D + (c % CPR) * 8) * sizeof(T));
-      kr[k] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-      vr[k] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+    for (int k = 0; k < LPT; ++k) {
+      const int pg = min(page_of(t, k), npages - 1);
+      ids[k] = __builtin_amdgcn_readfirstlane(kv_indices[pbase + pg]);
     }
   };
-  auto stage = [&](int t, const vec8* kr, const vec8* vr) {
-    unsigned char* kl = lds_tile(t & 1, 0);
-    unsigned char* vl = lds_tile(t & 1, 1);
+  auto load_tile = [&](int t, const int* ids, unsigned char* dst) {
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int c = tid + NT * k;
-      const int off = (c / CPR) * RSB + (c % CPR) * 16;
-      *reinterpret_cast<vec8*>(kl + off) = kr[k];
-      *reinterpret_cast<vec8*>(vl + off) = vr[k];
+    for (int k = 0; k < LPT; ++k) {
+      const int c0 = (k * 4 + wave) * 64;            // first chunk of this wave load
+      const int row0 = c0 / CPR;
+      const int pg = page_of(t, k);
+      const int raw = ids[k];
+      const bool bad = raw < 0 || (int64_t)raw >= num_blocks;
+      if (bad && pg < npages && lane == 0) flag(status, PKV_STATUS_BAD_PAGE);
+      const int live_rows = bad ? 0 : min(PS, kv_len - pg * PS);   // <= 0 past the end
+      const int64_t pid = bad ? 0 : raw;
+      const uint32_t range = live_rows > 0 ? (uint32_t)live_rows * rowbytes : 0u;
+      const __amdgpu_buffer_rsrc_t rk =
+          ws_rsrc(const_cast<T*>(kpool) + pid * PS * row, range);
+      const __amdgpu_buffer_rsrc_t rv =
+          ws_rsrc(const_cast<T*>(vpool) + pid * PS * row, range);
+      const int rr = row0 + lane / CPR;              // the lane's row of the tile
+      const int lc = (((lane % CPR) ^ xr(rr)) & 7) | ((lane % CPR) & ~7);  // its chunk
+      const uint32_t off = (uint32_t)((t * TT + rr) % PS) * rowbytes +
+                           (uint32_t)(h * RB + lc * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rk, (__attribute__((address_space(3))) void*)(dst + c0 * 16), 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (__attribute__((address_space(3))) void*)(dst + L::TILE + c0 * 16), 16, off, 0,
+          0, 0);
     }
   };
 
@@ -157,23 +196,60 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
   const int vrow = lane & 15;
   const int vcol = (lane & 16) + 4 * (vrow & 3);
 
-  auto compute = [&](int t) {
-    const unsigned char* kl = lds_tile(t & 1, 0);
-    const unsigned char* vl = lds_tile(t & 1, 1);
+  // P^T of the previous tile (the B operand of its PV), kept for the next step.
+  vec8 pb[NH * 2];
+#pragma unroll
+  for (int i = 0; i < NH * 2; ++i) pb[i] = vec8{};
+  // O^T += V^T P^T for a tile: V^T as the A operand, lane (dim, g) holding
+  // V[key][dim] for keys 16 kb + 4 g + 0..3 and 16 kb + 8 + 4 g + 0..3.
+  auto read_v = [&](const unsigned char* vl, vec8* va) {
+#pragma unroll
+    for (int kb = 0; kb < NH * 2; ++kb) {
+      const int key = 16 * kb + 4 * g + (vrow >> 2);
+#pragma unroll
+      for (int dh = 0; dh < NDH; ++dh) {
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(vl + swz<RB>(key, vcol + 32 * dh)));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(vl + swz<RB>(key + 8, vcol + 32 * dh)));
+        va[kb * NDH + dh] = __builtin_bit_cast(
+            vec8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    }
+  };
+  auto pv_mma = [&](const vec8* va) {
+#pragma unroll
+    for (int kb = 0; kb < NH * 2; ++kb) {
+#pragma unroll
+      for (int dh = 0; dh < NDH; ++dh) o[dh] = Mma32<T>::mma(va[kb * NDH + dh], pb[kb], o[dh]);
+    }
+  };
+  auto pv = [&](const unsigned char* vl) {
+    vec8 va[NH * 2 * NDH];
+    read_v(vl, va);
+    pv_mma(va);
+  };
+
+  // Tile t: S^T = K Q^T, then its softmax beside the previous tile's PV
+  // (independent of it), which leaves tile t's probabilities in pb.
+  auto compute = [&](int t, const unsigned char* kl, const unsigned char* vprev) {
     const int t0 = t * TT;
     const bool full = t0 + TT - 1 <= base_pos;
+    // the previous tile's V operands, read while QK runs
+    vec8 va[NH * 2 * NDH];
+    read_v(vprev, va);
     // S^T = K Q^T: s[hf][rr] = score of key t0 + 32 hf + 8 (rr / 4) + 4 g + rr % 4.
     f32x16 s[NH];
 #pragma unroll
     for (int hf = 0; hf < NH; ++hf) {
       s[hf] = f32x16{};
-      const unsigned char* kp = kl + (hf * 32 + n) * RSB + g * 16;
+      const int kr = hf * 32 + n;
 #pragma unroll
       for (int c = 0; c < NC; ++c)
-        s[hf] = Mma32<T>::mma(*reinterpret_cast<const vec8*>(kp + c * 32), qb[c], s[hf]);
+        s[hf] = Mma32<T>::mma(*reinterpret_cast<const vec8*>(kl + swz<RB>(kr, 16 * c + 8 * g)),
+                              qb[c], s[hf]);
     }
-    // Raw-score row max (scale_log2 > 0, so scaling commutes with max);
-    // keys past the row's position are masked only on tiles that reach them.
+    // Keys past the row's position are masked only on tiles that reach them.
     if (!full) {
 #pragma unroll
       for (int hf = 0; hf < NH; ++hf) {
@@ -184,6 +260,10 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
         }
       }
     }
+    // The previous tile's PV (zero probabilities before the first tile), its
+    // matrix instructions interleaved with the softmax's vector ones below.
+    pv_mma(va);
+    // Raw-score row max (scale_log2 > 0, so scaling commutes with max).
     float mx = -INFINITY;
 #pragma unroll
     for (int hf = 0; hf < NH; ++hf) {
@@ -191,9 +271,41 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
       for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, s[hf][rr]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+    // Probabilities against the running reference m_run, taken while the
+    // tile's max is still being reduced: 16-key block (hf, qq) of P^T uses
+    // the lane's scores rr = 8 qq .. 8 qq + 7 in that order.
+    float ls = 0.f;
+    auto probs = [&]() {
+      ls = 0.f;
+#pragma unroll
+      for (int hf = 0; hf < NH; ++hf) {
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hf][rr], scale_log2, -m_run));
+          ls += e;
+          pb[2 * hf + (rr >> 3)][rr & 7] = (T)e;
+        }
+      }
+    };
+    probs();
+    // (pinned here: otherwise the compiler moves them behind the max test)
+#pragma unroll
+    for (int i = 0; i < NH * 2; ++i) {
+      u32x4 w = __builtin_bit_cast(u32x4, pb[i]);
+      asm volatile("" : "+v"(w));
+      pb[i] = __builtin_bit_cast(vec8, w);
+    }
+    asm volatile("" : "+v"(ls));
+#pragma unroll
+    for (int i = 0; i < NH * 2 * NDH; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // then vector work
+    }
     // Lazy rescale: the reference max only moves when a row's max grows by
     // more than 2^8 (then p <= 256, exact in the pool dtype's range); the
-    // result o / l does not depend on which reference is used.
+    // result o / l does not depend on which reference is used. When it
+    // moves (always on the first tile), o (with the previous tile's PV
+    // added) and l are rescaled and the probabilities taken again.
     if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f)) {
       const float m_new = fmaxf(m_run, mx);   // finite: key 0 is visible to every row
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -201,61 +313,58 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
       m_run = m_new;
 #pragma unroll
       for (int dh = 0; dh < NDH; ++dh) o[dh] *= alpha;
+      probs();
     }
-    // P^T as the B operand of O^T = V^T P^T: 16-key block (hf, qq) uses
-    // the lane's scores rr = 8 qq .. 8 qq + 7 in that order.
-    vec8 pb[NH * 2];
-    float ls = 0.f;
-#pragma unroll
-    for (int hf = 0; hf < NH; ++hf) {
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hf][rr], scale_log2, -m_run));
-        ls += e;
-        pb[2 * hf + (rr >> 3)][rr & 7] = (T)e;
-      }
-    }
-    ls += __shfl_xor(ls, 32, 64);
+    // l_run: this lane's half of its row's keys; the halves meet at the end
     l_run += ls;
-#pragma unroll
-    for (int kb = 0; kb < NH * 2; ++kb) {
-      // V^T as the A operand: lane (dim, g) holds V[key][dim] for keys
-      // 16 kb + 4 g + 0..3 and 16 kb + 8 + 4 g + 0..3.
-      const unsigned char* vp = vl + (16 * kb + 4 * g + (vrow >> 2)) * RSB + vcol * (int)sizeof(T);
-#pragma unroll
-      for (int dh = 0; dh < NDH; ++dh) {
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(vp + 32 * dh * sizeof(T)));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(vp + 8 * RSB + 32 * dh * sizeof(T)));
-        const vec8 va = __builtin_bit_cast(
-            vec8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        o[dh] = Mma32<T>::mma(va, pb[kb], o[dh]);
-      }
-    }
   };
 
-  vec8 kA[CPT], vA[CPT], kB[CPT], vB[CPT];
-  load_tile(0, kA, vA);
-  load_tile(1, kB, vB);
-  stage(0, kA, vA);
-  load_tile(2, kA, vA);
-  __syncthreads();
-  // two register sets, so unrolled by two; re-entered only after the
-  // second half, so both halves' loads are in flight there
-  for (int t = 0;; t += 2) {
-    if (t + 1 < ntiles) stage(t + 1, kB, vB);
-    load_tile(t + 3, kB, vB);
-    compute(t);
-    __syncthreads();
+  // The ring: tile t in buffer t % 4. Each step waits for its tile's loads
+  // (this wave's, then every wave's at the barrier, which also ends every
+  // wave's reads of the buffer the step then refills: the one of tile t - 2,
+  // whose PV ran in the previous step), loads the pages of tile t + 2,
+  // computes tile t beside the PV of tile t - 1, and loads the page ids of
+  // tile t + 3.
+  int ids0[LPT], ids1[LPT], ids2[LPT], ids3[LPT];   // page ids of tile j in ids(j % 4)
+  load_ids(0, ids0);
+  load_ids(1, ids1);
+  __syncthreads();   // the zeroed ring before any load lands in it
+  load_tile(0, ids0, buf0);
+  load_ids(2, ids2);
+  load_tile(1, ids1, buf1);
+  auto step = [&](int t, unsigned char* cur, unsigned char* prev, unsigned char* nxt2,
+                  int* ids_t2, int* ids_t3) {
+    // Every tile load but the latest step's has landed; after the barrier,
+    // every wave's have. (A fenced barrier would wait for all of them.)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPT) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    load_tile(t + 2, ids_t2, nxt2);
+    compute(t, cur, prev + L::TILE);
+    // (after the tile's LDS reads: a scalar load in flight would make every
+    // wait for them a wait for it too)
+    load_ids(t + 3, ids_t3);
+  };
+  unsigned char* last = buf0;   // the buffer of the last tile computed
+  for (int t = 0;; t += 4) {
+    step(t, buf0, buf3, buf2, ids2, ids3);
+    last = buf0;
     if (t + 1 >= ntiles) break;
-    if (t + 2 < ntiles) stage(t + 2, kA, vA);
-    load_tile(t + 4, kA, vA);
-    compute(t + 1);
-    __syncthreads();
+    step(t + 1, buf1, buf0, buf3, ids3, ids0);
+    last = buf1;
     if (t + 2 >= ntiles) break;
+    step(t + 2, buf2, buf1, buf0, ids0, ids1);
+    last = buf2;
+    if (t + 3 >= ntiles) break;
+    step(t + 3, buf3, buf2, buf1, ids1, ids2);
+    last = buf3;
+    if (t + 4 >= ntiles) break;
   }
+  pv(last + L::TILE);   // the last tile's PV
+  // the loads of the tiles past the end land in LDS before the workgroup ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  l_run += __shfl_xor(l_run, 32, 64);
   if (valid) {
     const float inv = 1.f / l_run;
     T* orow = out + ((int64_t)(q0 + qs + tok) * Hq + h * G + r % G) * D + 4 * g;
@@ -277,9 +386,7 @@ static void launch_prefill(const void* q, void* out, const void* kp, const void*
                            const int32_t* cu_q, const int32_t* indptr, const int32_t* indices,
                            const int32_t* kv_lens, const int32_t* plan, int32_t n_tiles,
                            int32_t Hkv, float sl2, int32_t* status, hipStream_t s) {
-  constexpr int TT = 32;
-  const size_t lds = 2 * 2 * TT * (D * sizeof(T) + 16);  // two K+V tiles of TT padded rows
-  hipLaunchKernelGGL((prefill_kernel<T, D, G>), dim3((unsigned)(n_tiles * Hkv)), dim3(kPrefillThreads), lds,
+  hipLaunchKernelGGL((prefill_kernel<T, D, G>), dim3((unsigned)(n_tiles * Hkv)), dim3(kPrefillThreads), 0,
                      s, (const T*)q, (T*)out, (const T*)kp, (const T*)vp, nb, cu_q, indptr,
                      indices, kv_lens, plan, Hkv, sl2, status);
 }

@@ -162,6 +162,38 @@ def test_chunked_prefill_over_shared_prefix(geom, dtype):
     check(p.step(meta, 6, kv_scale=0.5), "chunk over shared prefix", tol, rtol)
 
 
+@pytest.mark.parametrize("lens,hist", [([int(x) for x in np.random.default_rng(5).integers(1, 64, 300)], 0),
+                                       ([300, 517, 64, 1000], 700)])
+def test_prefill_bits_do_not_change_between_runs(lens, hist):
+    """The prefill kernel's K/V tile ring (direct-to-LDS loads, one barrier
+    a tile) gives the same bits on every run: a tile read before its loads
+    have landed, or a buffer refilled while still read, shows up as
+    run-to-run differences. Short sequences (one or two tiles each, many
+    workgroups ending early) and chunks over a long history."""
+    print(f"prefill determinism: {len(lens)} sequences, history {hist}", flush=True)
+    bk = MI355XBackend(1, 2048, 16, 8, 32, 64, device=DEV)
+    alloc = BlockAllocator(2048, 16)
+    alloc.allocate(2048)
+    alloc.free(torch.randperm(2048, generator=torch.Generator().manual_seed(3)).tolist())
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(len(lens))]
+    g = torch.Generator(device=DEV).manual_seed(4)
+    if hist:
+        h = _to_dev(grow_and_assemble(seqs, [hist] * len(lens), 16))
+        kv = [(torch.randn(h.n_tokens, 8, 64, generator=g, device=DEV) * 0.5).half()
+              for _ in range(2)]
+        bk.append_kv(0, kv[0], kv[1], h)
+    meta = _to_dev(grow_and_assemble(seqs, lens, 16))
+    T = meta.n_tokens
+    k, v = [(torch.randn(T, 8, 64, generator=g, device=DEV) * 0.5).half() for _ in range(2)]
+    q = (torch.randn(T, 32, 64, generator=g, device=DEV) * 0.5).half()
+    bk.append_kv(0, k, v, meta)
+    first = bk.attend(q, 0, 0.125, meta)
+    for i in range(10):
+        again = bk.attend(q, 0, 0.125, meta)
+        assert torch.equal(first, again), f"run {i + 1} differs from the first"
+    bk.check_device_errors()
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_matrix_core_prefill_matches_generic_kernel(dtype):
     """Same batch through the MFMA prefill (default tile) and the generic
