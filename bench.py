@@ -31,6 +31,8 @@ Other workloads (one JSON line each, same fields):
   capacity  decode at 4096 sequences of 16..64 tokens, then 512 sequences of
             lognormal mean 2048 (clipped to 2048), pool of ~200 GB; GB/s.
   calib     a 1 GiB device copy, the known-size reference for HBM counters.
+  argmax    greedy sampling of a decode step's logits on the device: 256 rows
+            of Llama-3's 128 256-entry vocabulary, fp16; GB/s of the read.
   timeline  the headline decode launch under the instrumented build
             (``python -m llm_serving_layer_amd.build --timeline``, loaded with
             PKV_LIBRARY=llm_serving_layer_amd/_native/libpagedkv_timeline.so):
@@ -439,6 +441,44 @@ def cpu_baseline(lens, budget_s=10.0):
                               "sample": f"{n1} passes, median {one_s * 1e3:.1f} ms/layer"}}
 
 
+# ------------------------------------------------------------------ argmax ---
+
+def bench_argmax(args):
+    """pkv_argmax_rows over (256, 128256) fp16 logits, the greedy pick of a
+    batch-256 decode step (torch.argmax(logits, dim=-1) in the reference's
+    scheduler), checked against torch.argmax outside the timed region."""
+    import torch
+    from llm_serving_layer_amd.sampling import greedy
+
+    rows, vocab = 256, 128256
+    g = torch.Generator(device="cuda:0").manual_seed(SEED)
+    x = (torch.randn(rows, vocab, generator=g, device="cuda:0") * 4).half()
+    if not torch.equal(greedy(x), torch.argmax(x, dim=-1)):
+        raise RuntimeError("greedy ids differ from torch.argmax")
+    for _ in range(args.warmup):
+        greedy(x)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(args.steps):
+        greedy(x)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    nbytes = rows * vocab * 2 + rows * 8
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    line = base_line(args, "greedy argmax HBM GB/s, 1 GPU", round(gbps, 1), "GB/s", ms, "fp16",
+                     f"greedy sampling: argmax of {rows} rows x {vocab} fp16 logits",
+                     rows=rows, vocab=vocab)
+    line.update({"roofline": {"kernel": "pkv::argmax_kernel<_Float16>", "bound": "hbm",
+                              "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                              "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                              "algorithmic_bytes_per_launch": nbytes,
+                              "avg_launch_ms": round(ms, 5),
+                              "timing": "HIP events around K launches on the current stream"}})
+    return line
+
+
 # ---------------------------------------------------------------- timeline ---
 
 def bench_timeline(args):
@@ -820,7 +860,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "prefill", "copy", "swap", "capacity", "calib",
-                             "timeline"])
+                             "timeline", "argmax"])
     ap.add_argument("--part-pages", type=int, default=None,
                     help="split-K partition size in pages (default: the backend's)")
     ap.add_argument("--eager", action="store_true",
@@ -838,7 +878,7 @@ def main() -> int:
         args.part_pages = DEFAULT_PART_PAGES
     fn = {"decode": bench_decode, "prefill": bench_prefill, "copy": bench_copy,
           "swap": bench_swap, "capacity": bench_capacity, "calib": bench_calib,
-          "timeline": bench_timeline}[args.workload]
+          "timeline": bench_timeline, "argmax": bench_argmax}[args.workload]
     print(json.dumps(fn(args)))
     return 0
 

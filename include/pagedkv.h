@@ -270,6 +270,18 @@ int pkv_scatter_blocks(void* pool_base, int32_t n_layers, int64_t plane_bytes,
                        const int32_t* ids, int32_t n_ids, const void* staging,
                        int32_t* status_word, void* stream);
 
+/*
+ * Greedy sampling — the scheduler's torch.argmax(logits, dim=-1)
+ * (serving/scheduler/scheduler.py:752-757) on the device: out_ids[r] = the
+ * index of the largest of the `vocab` logits of row r (row r starts at
+ * element r * row_stride), with torch's order: a NaN beats every number
+ * and between equal values the smaller index wins. logits are f16, bf16 or
+ * f32 (dtype); out_ids is a device int64 array of n_rows entries. n_rows = 0
+ * does nothing.
+ */
+int pkv_argmax_rows(const void* logits, int64_t n_rows, int64_t vocab, int64_t row_stride,
+                    int32_t dtype, int64_t* out_ids, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,6 +10,8 @@ hand-written gfx950 kernels (include/pagedkv.h, csrc/):
 * ``backend``   — MI355XBackend (append_kv / attend / copy_block[s]);
 * ``swap``      — KVSwapSpace / SwapHandle (preemption swap);
 * ``sizing``    — plan_kv_pool / KVPoolPlan (pool sizing for one MI355X).
+* ``sampling``  — greedy (argmax on the device), StepTimer, greedy_step (the
+  scheduler step's forward-and-sample part, timed with HIP events).
 """
 
 from .assembly import ScheduledSeq, build_batch_meta, build_token_tensor

@@ -146,7 +146,7 @@ using namespace pkv;
 
 extern "C" {
 
-int pkv_abi_version(void) { return 9; }
+int pkv_abi_version(void) { return 10; }
 
 const char* pkv_last_error(void) { return g_err.c_str(); }
 

@@ -19,6 +19,8 @@ or with the op-for-op restatement:
   - ``gather_closed_form`` / ``scatter_closed_form``: the swap copies
     ``host[l] = pool[l][ids]`` and ``pool[l][ids] = host[l]``
     (serving/scheduler/preemption.py:490-523).
+* ``greedy_ids``: the scheduler's greedy pick, ``torch.argmax(logits,
+  dim=-1)`` (serving/scheduler/scheduler.py:752-757), as an explicit scan.
 """
 
 from __future__ import annotations
@@ -28,7 +30,7 @@ import math
 import numpy as np
 
 __all__ = ["naive_attention", "append_closed_form", "copy_blocks_closed_form",
-           "gather_closed_form", "scatter_closed_form"]
+           "gather_closed_form", "scatter_closed_form", "greedy_ids"]
 
 
 def naive_attention(q: np.ndarray, k_full: np.ndarray, v_full: np.ndarray,
@@ -89,3 +91,27 @@ def scatter_closed_form(pools: list, host: np.ndarray, ids) -> list:
         for i, b in enumerate(ids):
             p[int(b)] = host[layer, i]
     return out
+
+
+
+def greedy_ids(logits) -> list[int]:
+    """
+    The greedy token of every row of ``logits`` (n_rows, vocab), the order
+    torch.argmax(logits, dim=-1) uses (serving/scheduler/scheduler.py:
+    752-757): a NaN beats every number (torch's max reductions propagate
+    NaN), a larger value beats a smaller one, and of equal values the first
+    wins. An explicit scan over each row, in float64.
+    """
+    out = []
+    for row in np.asarray(logits, dtype=np.float64):
+        best, bi = None, -1
+        for i, v in enumerate(row.tolist()):
+            if bi < 0:
+                best, bi = v, i
+            elif math.isnan(best):
+                continue
+            elif math.isnan(v) or v > best:
+                best, bi = v, i
+        out.append(bi)
+    return out
+

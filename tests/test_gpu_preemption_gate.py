@@ -75,6 +75,50 @@ class ToyModel:
         return [int(np.argmax(h[i] @ self.head)) for i in last]
 
 
+class DeviceToyModel(ToyModel):
+    """The same model on the GPU, driven the way the reference's scheduler
+    drives its model (serving/scheduler/scheduler.py:743-757): ``forward``
+    is ``greedy_step`` (metadata, token ids, ``forward_varlen`` returning
+    device logits, greedy ids picked on the device, one copy of the ids to
+    the host), timed with HIP events. Every projection runs one token row at
+    a time in float32 with the same matrix shapes whatever the batch, so a
+    row's logits cannot depend on what it is batched with."""
+
+    def __init__(self, seed=11, device="cuda:0"):
+        super().__init__(seed)
+        dev = torch.device(device)
+        f = lambda a: torch.from_numpy(np.asarray(a, dtype=np.float32)).to(dev)  # noqa: E731
+        self.d_emb, self.d_head = f(self.emb), f(self.head)
+        self.d_w = [[f(w[l]) for l in range(LAYERS)] for w in (self.wq, self.wk, self.wv, self.wo)]
+        from llm_serving_layer_amd.sampling import StepTimer
+        self.timer = StepTimer(dev)
+        self.step_ms = []
+
+    @staticmethod
+    def drows(x, w):
+        return torch.cat([x[i:i + 1] @ w for i in range(x.shape[0])])
+
+    def forward_varlen(self, tokens, meta, backend):
+        h = self.d_emb[tokens]
+        n = tokens.shape[0]
+        wq, wk, wv, wo = self.d_w
+        for layer in range(LAYERS):
+            q = self.drows(h, wq[layer]).reshape(n, HQ, D).to(backend.dtype)
+            k = self.drows(h, wk[layer]).reshape(n, HKV, D).to(backend.dtype)
+            v = self.drows(h, wv[layer]).reshape(n, HKV, D).to(backend.dtype)
+            backend.append_kv(layer, k, v, meta)
+            o = backend.attend(q, layer, D ** -0.5, meta).float().reshape(n, HQ * D)
+            h = h + self.drows(o, wo[layer])
+        last = meta.cu_query_lens[1:].long() - 1
+        return self.drows(h[last], self.d_head)
+
+    def forward(self, backend, scheduled):
+        from llm_serving_layer_amd.sampling import greedy_step
+        ids = greedy_step(self, scheduled, backend, BS, self.timer)
+        self.step_ms.append(self.timer.elapsed_ms())
+        return ids
+
+
 def generate(model, preempt: bool, policy: str = "swap", dtype=torch.float16):
     """Run every prompt to NEW_TOKENS tokens. With ``preempt`` the victims are
     swapped out at decode step SWAP_AT and their blocks freed; those blocks
@@ -166,3 +210,22 @@ def test_greedy_tokens_are_bit_identical_under_preemption(policy, dtype):
     for i, (a, b) in enumerate(zip(ref, got)):
         assert a == b, f"request {i}: {a} unpreempted vs {b} under preemption"
     assert len({t for o in ref for t in o}) > 3, "tokens should not be trivially constant"
+
+
+@pytest.mark.parametrize("policy", ["swap", "recompute"])
+def test_greedy_step_on_device_is_bit_identical_under_preemption(policy):
+    """The gate through the scheduler's step structure on the device: greedy
+    ids picked by the library's argmax kernel from device logits, each step
+    timed with HIP events; swap and recompute (fp32 pools) both give the
+    unpreempted tokens."""
+    print(f"device greedy-step gate policy={policy}", flush=True)
+    dtype = torch.float16 if policy == "swap" else torch.float32
+    model = DeviceToyModel()
+    ref, _ = generate(model, preempt=False, dtype=dtype)
+    got, info = generate(model, preempt=True, policy=policy, dtype=dtype)
+    assert set(info["moved"]) == set(VICTIMS) and info["steps"] > RESUME_AT
+    for i, (a, b) in enumerate(zip(ref, got)):
+        assert a == b, f"request {i}: {a} unpreempted vs {b} under preemption"
+    assert len({t for o in ref for t in o}) > 3, "tokens should not be trivially constant"
+    assert len(model.step_ms) > 2 * NEW_TOKENS and all(ms > 0 for ms in model.step_ms)
+

@@ -1,0 +1,66 @@
+"""
+Greedy sampling, host side: the oracle's scan (oracle/naive.py greedy_ids)
+pinned against the reference's own call, torch.argmax(logits, dim=-1)
+(serving/scheduler/scheduler.py:752-757), on rows built to separate the
+plausible orders (ties, NaN, infinities), with a planted last-of-ties
+variant that must fail; and ``greedy``'s argument checks, which run before
+the library is touched.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import greedy_ids
+
+from llm_serving_layer_amd import sampling
+
+
+def _rows():
+    nan, inf = math.nan, math.inf
+    fixed = [
+        [1.0, 3.0, 3.0, 2.0],            # tie: the first of the two
+        [5.0, 1.0, 2.0, 5.0],            # tie at both ends
+        [nan, 1.0, nan, 5.0],            # NaN first: it wins
+        [1.0, 5.0, nan, 9.0],            # NaN later beats the larger 9
+        [-inf, -inf, -inf, -inf],        # all -inf: index 0
+        [inf, 2.0, inf, 1.0],            # two +inf: the first
+        [-1.0, -0.5, -0.5, -2.0],
+        [0.0, -0.0, 0.0, 0.0],           # signed zeros are equal
+    ]
+    rng = np.random.default_rng(7)
+    rand = rng.standard_normal((6, 257)).astype(np.float32)
+    rand[1, 200] = rand[1, 3] = rand[1].max() + 1      # planted tie of the max
+    rand[2, 100] = nan
+    return [np.array(r, dtype=np.float32) for r in fixed] + list(rand)
+
+
+def test_greedy_ids_equal_torch_argmax():
+    for row in _rows():
+        want = int(torch.argmax(torch.from_numpy(row)[None], dim=-1)[0])
+        assert greedy_ids(row[None]) == [want], f"row {row[:8]}"
+    big = np.random.default_rng(3).standard_normal((5, 1000)).astype(np.float16)
+    assert greedy_ids(big) == torch.argmax(torch.from_numpy(big).float(), dim=-1).tolist()
+
+
+def test_planted_last_of_ties_order_is_caught():
+    """A restatement that keeps the last of equal maxima must disagree with
+    the reference on the tie rows above."""
+    def last_of_ties(rows):
+        return [len(r) - 1 - int(np.argmax(np.asarray(r)[::-1])) for r in rows]
+    rows = np.array([[1.0, 3.0, 3.0, 2.0], [5.0, 1.0, 2.0, 5.0]], dtype=np.float32)
+    assert last_of_ties(rows) != torch.argmax(torch.from_numpy(rows), dim=-1).tolist()
+    assert greedy_ids(rows) == torch.argmax(torch.from_numpy(rows), dim=-1).tolist()
+
+
+@pytest.mark.parametrize("bad, match", [
+    (torch.zeros(4), "must be \\(n_rows, vocab\\)"),
+    (torch.zeros(2, 3), "on the GPU"),
+])
+def test_greedy_rejects_bad_logits_before_launching(bad, match):
+    with pytest.raises(ValueError, match=match):
+        sampling.greedy(bad)
