@@ -18,8 +18,15 @@
 //  * Waves. Each wave owns one KV head and runs the bin's page stream on its
 //    own (no workgroup barrier anywhere): it loads its head's 128-byte slice
 //    of every token row (whole cache lines, eight lanes a row) into registers
-//    three pages ahead of use, copies the page to its private LDS tile, and
-//    reads the tile back in the matrix-core operand layouts.
+//    one page ahead of use, copies the page to its private LDS tile, and
+//    reads the tile back in the matrix-core operand layouts. One page in
+//    flight per wave measured faster than two or three: with 2048 waves
+//    streaming, deeper prefetch only lengthens the queue at the memory
+//    system (the first page lands later, and the stream is no faster).
+//    Every step issues the same loads on every path (no page skipped at the
+//    end of the stream, Q and new rows staged in LDS per batch of items,
+//    page words read with scalar loads), so the wait for a page never waits
+//    for the page issued after it.
 //
 // Per wave, head and page (G query heads share the KV head, G <= 16):
 //  1. S^T = K Q^T with one 16x16x32 MFMA per 32 dims: the K rows (from LDS)
@@ -71,9 +78,6 @@ constexpr int kItemInts = 8;        // {seq, n_pages, first token, kv_len, slot,
                                     //  first slot, flags}
 constexpr int kItemLast = 1;        // flags: the piece holds its sequence's last page
 constexpr int kPlanTail = 64;       // zero ints after the last bin (whole-wave word loads)
-// Pages in flight per wave beyond the one in use: three where registers
-// allow (head_dim 64, up to 4 query heads per KV head), else two.
-constexpr int depth_for(int D, int G) { return D > 64 || G > 4 ? 2 : 3; }
 
 // KV heads per workgroup: one wave each, at most kMaxWaves, dividing Hkv.
 static int heads_per_wg(int hkv) { return hkv % 4 == 0 ? 4 : hkv % 2 == 0 ? 2 : 1; }
@@ -217,6 +221,20 @@ template <typename T, int D> struct Tile {
   static constexpr int BYTES = 2 * 16 * RS;
 };
 
+// A wave's item slots in LDS: C items of {Q rows of the G query heads of
+// its KV head, the KV head's slice of the new K row, of the new V row}.
+template <typename T, int D, int G> struct Stage {
+  static constexpr int QB = G * D * (int)sizeof(T);
+  static constexpr int RB = D * (int)sizeof(T);
+  static constexpr int SLOT = QB + 2 * RB;
+  static constexpr int C = 4096 / QB < 1 ? 1 : 4096 / QB > 8 ? 8 : 4096 / QB;
+  static constexpr int QC = QB / 16;          // 16-byte chunks of the Q rows
+  static constexpr int RC = RB / 16;          // of a new row slice
+  static constexpr int CPI = SLOT / 16;       // per slot
+  static constexpr int ROUNDS = (C * CPI + 63) / 64;
+  static constexpr int BYTES = C * SLOT;
+};
+
 // One workgroup per (bin, group of KV heads); wave w streams KV head
 // hg * waves + w through the bin's pages, one piece (item) after another,
 // without restarting the page pipeline at item boundaries. The bin's plan
@@ -226,9 +244,9 @@ template <typename T, int D> struct Tile {
 //
 // Cut sequences. A piece that is not its sequence's last publishes its
 // partial (o, m, l) with sc1 stores and goes on streaming; its arrival is
-// counted kDepth + 1 pages later, when the wait for a page loaded after those
+// counted two pages later, when the wait for a page loaded after those
 // stores has (vmcnt counts in order) also seen the stores complete, and the
-// count it returns is checked kDepth pages after that. The last piece of a
+// count it returns is checked at once. The last piece of a
 // cut sequence runs at the end of its bin: it reads the arrival counter when
 // it starts and, if every other piece has arrived by then, merges at its end
 // without counting itself (it publishes its own partial first, so both paths
@@ -255,9 +273,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   constexpr int RS = TL::RS;
   constexpr int NGR = PL::NGR;
   constexpr int OPS = 2 * NLD;         // vector memory instructions per page load
-  constexpr int kDepth = depth_for(D, G);
   static_assert(NLD * RPI == PS && CPR * RPI == 64, "a wave loads whole head rows");
-  static_assert(OPS * (kDepth - 1) < 64, "vmcnt field");
 
   extern __shared__ __align__(16) unsigned char smem[];
   PKV_TL(const unsigned long long tl_start = __builtin_amdgcn_s_memrealtime();
@@ -280,10 +296,6 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   const int n_items = bp[0], n_pages = bp[1];
   const int32_t* words = bp + kHdrInts;
   const int32_t* items = words + ((n_pages + 3) & ~3);
-  // Lane l holds page word 64c + l of chunk c: even chunks in pw0, odd in
-  // pw1. The whole-wave load may run past the bin's words; the plan is
-  // padded so it stays inside the buffer (those lanes are never used).
-  int pw0 = words[lane], pw1 = 0;
   if (n_items <= 0) return;
 
   // This lane's chunk of a page: row k * RPI + lane / CPR, bytes
@@ -291,13 +303,12 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   // load instruction reads whole cache lines.
   const int lrow0 = lane / CPR;
   const uint32_t lcol = (uint32_t)(lane % CPR) * 16;
-  auto word_of = [&](int p) -> int {   // p is wave-uniform
-    return __builtin_amdgcn_readlane(((p >> 6) & 1) ? pw1 : pw0, p & 63);
-  };
-  auto load_page = [&](int p, vec8* kr, vec8* vr) {
-    const int w = word_of(p);
-    const int64_t page = w & ((1 << kPageIdBits) - 1);
-    const uint32_t live = (((uint32_t)w >> kPageIdBits) & 15u) + 1u;
+  // Page p of the stream (p wave-uniform, word w = words[p]); past the
+  // bin's last page every load is outside its range: no access, zeros.
+  auto load_page = [&](int p, int w, vec8* kr, vec8* vr) __attribute__((always_inline)) {
+    const bool in = p < n_pages;
+    const int64_t page = in ? (w & ((1 << kPageIdBits) - 1)) : 0;
+    const uint32_t live = in ? (((uint32_t)w >> kPageIdBits) & 15u) + 1u : 0u;
     const __amdgpu_buffer_rsrc_t rk = ws_rsrc(kpool + page * PS * row_elems, live * frow);
     const __amdgpu_buffer_rsrc_t rv = ws_rsrc(vpool + page * PS * row_elems, live * frow);
 #pragma unroll
@@ -307,52 +318,87 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       vr[k] = __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, kNt));
     }
   };
-  vec8 kr[kDepth][NLD], vr[kDepth][NLD];
-#pragma unroll
-  for (int s = 0; s < kDepth; ++s)
-    if (s < n_pages) load_page(s, kr[s], vr[s]);
-
-  // ---- items: the current one in scalars, the next one's Q (and new row)
-  // loaded one item ahead.
+  // ---- items: fields from the plan (scalar loads); Q and the new row of
+  // SG::C items at a time staged in this wave's LDS slots, loaded in one
+  // batch (the first batch before the first pages, so waiting for it never
+  // waits for a page).
   struct Item { int seq, np, tok0, kv, slot, nparts, slot0, flags; };
-  auto item_at = [&](int i) -> Item {
+  auto item_at = [&](int i) __attribute__((always_inline)) -> Item {
     const int32_t* it = items + (int64_t)i * kItemInts;
     return Item{it[0], it[1], it[2], it[3], it[4], it[5], it[6], it[7]};
   };
-  // Q^T as the QK B operand: column n = query head h*G + n (zero beyond G).
-  auto load_q = [&](vec8* dst, int sq) {
-    const T* qr = q + ((int64_t)sq * Hq + h * G + (n < G ? n : 0)) * D + g * 8;
+  const bool fuse = k_new != nullptr;
+  typedef Stage<T, D, G> SG;
+  unsigned char* stg = smem + hgw * TL::BYTES + wave * SG::BYTES;
+  // Loads of the slots of items i0 .. i0 + C - 1: lane chunk c = 64 r + lane
+  // is 16 bytes w of item i's slot (Q rows of the KV head's G query heads,
+  // then the KV head's slice of the new K row and of the new V row).
+  auto stage_load = [&](int i0, u32x4* d) __attribute__((always_inline)) {
+    const int ns = min(SG::C, n_items - i0);
+    int sq[SG::C], fl[SG::C];
+#pragma unroll
+    for (int j = 0; j < SG::C; ++j) {
+      const int32_t* it = items + (int64_t)(i0 + min(j, ns - 1)) * kItemInts;
+      sq[j] = it[0];
+      fl[j] = it[7];
+    }
+#pragma unroll
+    for (int r = 0; r < SG::ROUNDS; ++r) {
+      const int c = r * 64 + lane;
+      const int i = c / SG::CPI, w = c - i * SG::CPI;
+      int si = sq[0], fi = fl[0];
+#pragma unroll
+      for (int j = 1; j < SG::C; ++j)
+        if (i == j) { si = sq[j]; fi = fl[j]; }
+      const unsigned char* src = nullptr;
+      if (i < ns) {
+        if (w < SG::QC)
+          src = reinterpret_cast<const unsigned char*>(q + ((int64_t)si * Hq + h * G) * D) + w * 16;
+        else if (fuse && (fi & kItemLast))
+          src = reinterpret_cast<const unsigned char*>(
+                    (w < SG::QC + SG::RC ? k_new : v_new) + (int64_t)si * row_elems + h * D) +
+                (w < SG::QC + SG::RC ? w - SG::QC : w - SG::QC - SG::RC) * 16;
+      }
+      d[r] = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto stage_store = [&](const u32x4* d) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < SG::ROUNDS; ++r) {
+      const int c = r * 64 + lane;
+      if (c < SG::C * SG::CPI) *reinterpret_cast<u32x4*>(stg + c * 16) = d[r];
+    }
+    wave_lds_sync();
+  };
+  u32x4 sgd[SG::ROUNDS];
+  stage_load(0, sgd);
+  // One page in flight: its registers and its word; the next page's word is
+  // read a step ahead.
+  vec8 kr[NLD], vr[NLD];
+  int wcur = words[0];
+  load_page(0, wcur, kr, vr);
+  int wnext = words[1];
+  stage_store(sgd);
+
+  Item cur = item_at(0);
+  vec8 qb[NCH], kx{}, vx{};
+  int new_slot = 0;
+  // Item i (slot i % C staged) becomes current: Q^T as the QK B operand
+  // (column n = query head h*G + n, zero beyond G) and this lane's 16 bytes
+  // of the new row.
+  auto take_item = [&](int i) __attribute__((always_inline)) {
+    const unsigned char* sl = stg + (i % SG::C) * SG::SLOT;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      vec8 t = *reinterpret_cast<const vec8*>(qr + c * 32);
-      dst[c] = (n < G) ? t : vec8{};
+      const vec8 t = *reinterpret_cast<const vec8*>(
+          sl + ((n < G ? n : 0) * D + c * 32 + g * 8) * (int)sizeof(T));
+      qb[c] = (n < G) ? t : vec8{};
     }
+    kx = *reinterpret_cast<const vec8*>(sl + SG::QB + lcol);
+    vx = *reinterpret_cast<const vec8*>(sl + SG::QB + RB + lcol);
+    new_slot = (fuse && (cur.flags & kItemLast)) ? slot_mapping[cur.seq] : 0;
   };
-  // This lane's 16 bytes of the new row (fused append).
-  auto load_new = [&](vec8& kx, vec8& vx, int sq) {
-    const unsigned char* kn = reinterpret_cast<const unsigned char*>(k_new + sq * row_elems);
-    const unsigned char* vn = reinterpret_cast<const unsigned char*>(v_new + sq * row_elems);
-    kx = *reinterpret_cast<const vec8*>(kn + h * RB + lcol);
-    vx = *reinterpret_cast<const vec8*>(vn + h * RB + lcol);
-  };
-  const bool fuse = k_new != nullptr;
-  Item cur = item_at(0);
-  vec8 qb[NCH], qn[NCH], kx{}, vx{}, kxn{}, vxn{};
-  int new_slot = 0, new_slot_n = 0;
-  load_q(qb, cur.seq);
-  if (fuse && (cur.flags & kItemLast)) {
-    load_new(kx, vx, cur.seq);
-    new_slot = slot_mapping[cur.seq];
-  }
-  Item nxt = cur;
-  if (n_items > 1) {
-    nxt = item_at(1);
-    load_q(qn, nxt.seq);
-    if (fuse && (nxt.flags & kItemLast)) {
-      load_new(kxn, vxn, nxt.seq);
-      new_slot_n = slot_mapping[nxt.seq];
-    }
-  }
+  take_item(0);
   int it_idx = 0;
   int it_start = 0, it_end = cur.np;   // the current item's pages in the stream
 
@@ -365,7 +411,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   const __amdgpu_buffer_rsrc_t rm = ws_rsrc(part_ml, ml_bytes);
 
   // lane (dim column n, group g) holds heads 4g..4g+3 of dims 16b + n.
-  auto write_out = [&](int sq) {
+  auto write_out = [&](int sq) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * g + i;
@@ -380,9 +426,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
 
   // The current item's last page: write the new row (fused append) and patch
   // the loaded copy when slot_mapping agrees with the page table.
-  auto append_row = [&](int p, vec8* kq, vec8* vq) {
+  auto append_row = [&](int w, vec8* kq, vec8* vq) __attribute__((always_inline)) {
     const int tl = (cur.kv - 1) % PS;  // newest token's row within its page
-    const int64_t page = word_of(p) & ((1 << kPageIdBits) - 1);
+    const int64_t page = w & ((1 << kPageIdBits) - 1);
     const bool in_range = new_slot >= 0 && (int64_t)new_slot < num_blocks * PS;
     if (!in_range) {
       if (lane == 0) flag(status, PKV_STATUS_BAD_SLOT);
@@ -405,7 +451,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   };
 
   // Merge (seq, h) from the stored partials and reset its counter.
-  auto merge = [&](int sq, int nparts, int slot0) {
+  auto merge = [&](int sq, int nparts, int slot0) __attribute__((always_inline)) {
     PKV_TL(const unsigned long long tm = __builtin_amdgcn_s_memrealtime(); ++tl_merges;)
     merge_head<T, D, G>(out, reinterpret_cast<float*>(kl), sq, h, n_kv_heads, nparts, slot0,
                         ro, rm);
@@ -415,33 +461,33 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     PKV_TL(tl_merge += __builtin_amdgcn_s_memrealtime() - tm;)
   };
   // Count an arrival whose partial has completed; the returned count.
-  auto arrive = [&](int sq) -> int {
+  auto arrive = [&](int sq) __attribute__((always_inline)) -> int {
     int old = 0;
     if (lane == 0)
       old = __hip_atomic_fetch_add(counters + (int64_t)sq * n_kv_heads + h, 1, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
     return old;
   };
-  // A deferred arrival: 0 none, 1 partial stored (count at page pa_at),
-  // 2 counted (check the returned count at page pa_at).
+  // A deferred arrival: pa_state 1 once a partial is stored; it is counted
+  // at page pa_at.
   int pa_state = 0, pa_at = 0, pa_seq = 0, pa_nparts = 0, pa_slot0 = 0, pa_old = 0;
-  auto finish_arrival = [&]() {   // check a counted arrival: the last one merges
+  // check a counted arrival: the last one merges
+  auto finish_arrival = [&]() __attribute__((always_inline)) {
     if (__builtin_amdgcn_readfirstlane(pa_old) == pa_nparts - 1)
       merge(pa_seq, pa_nparts, pa_slot0);
     pa_state = 0;
   };
-  auto flush_arrival = [&]() {    // complete a pending arrival now
+  auto flush_arrival = [&]() __attribute__((always_inline)) {  // count a pending arrival now
     if (pa_state == 1) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       pa_old = arrive(pa_seq);
-      pa_state = 2;
+      finish_arrival();
     }
-    if (pa_state == 2) finish_arrival();
   };
   int b_count = 0;   // the arrival counter as the last piece of a cut sequence found it
 
   // Item end: the output (whole sequence), or the partial of a cut sequence.
-  auto end_item = [&](int p) {
+  auto end_item = [&](int p) __attribute__((always_inline)) {
     if (cur.slot < 0) {
       write_out(cur.seq);
     } else {
@@ -473,10 +519,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
           pa_old = arrive(cur.seq);
           finish_arrival();
         }
-      } else if (p + 2 * kDepth < n_pages) {
+      } else if (p + 2 < n_pages) {
         // count it once a page loaded after the stores has arrived
         pa_state = 1;
-        pa_at = p + 1 + kDepth;
+        pa_at = p + 2;
         pa_seq = cur.seq;
         pa_nparts = cur.nparts;
         pa_slot0 = cur.slot0;
@@ -491,30 +537,22 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     }
     ++it_idx;
     if (it_idx < n_items) {
-      cur = nxt;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) qb[c] = qn[c];
-      kx = kxn;
-      vx = vxn;
-      new_slot = new_slot_n;
+      if (it_idx % SG::C == 0) {   // the next batch of slots
+        stage_load(it_idx, sgd);
+        stage_store(sgd);
+      }
+      cur = item_at(it_idx);
+      take_item(it_idx);
       it_start = it_end;
       it_end += cur.np;
       m_run = -INFINITY;
       l_run = 0.f;
 #pragma unroll
       for (int b = 0; b < NDB; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (it_idx + 1 < n_items) {
-        nxt = item_at(it_idx + 1);
-        load_q(qn, nxt.seq);
-        if (fuse && (nxt.flags & kItemLast)) {
-          load_new(kxn, vxn, nxt.seq);
-          new_slot_n = slot_mapping[nxt.seq];
-        }
-      }
     }
   };
 
-  auto compute = [&](int p) {
+  auto compute = [&](int p) __attribute__((always_inline)) {
     const int tp = cur.tok0 + (p - it_start) * PS;  // first token of the page
     // S^T: lane (n, g) gets the scores of tokens 4g..4g+3 for head n.
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -566,56 +604,40 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     }
   };
 
-  // Page p sits in register set p % kDepth. Step p stages it into the
-  // wave's tile (patched with the new row at a sequence's last page), refills
-  // its registers with page p + kDepth, and computes page p.
-  for (int p0 = 0; p0 < n_pages; p0 += kDepth) {
+  // Step p: stage page p into the wave's tile (patched with the new row at
+  // a sequence's last page), send the loads of page p + 1 into the same
+  // registers, then compute page p. Every step issues exactly one page's
+  // loads (past the bin's last page: no access), so on every path through
+  // the loop the wait for page p counts only page p's loads.
+  for (int p = 0; p < n_pages; ++p) {
+    if (fuse && (cur.flags & kItemLast) && p == it_end - 1) append_row(wcur, kr, vr);
+    if (wcur < 0 && lane == 0) flag(status, PKV_STATUS_BAD_PAGE);
 #pragma unroll
-    for (int s = 0; s < kDepth; ++s) {
-      const int p = p0 + s;
-      if (p < n_pages) {
-        if (fuse && (cur.flags & kItemLast) && p == it_end - 1) append_row(p, kr[s], vr[s]);
-        if (word_of(p) < 0 && lane == 0) flag(status, PKV_STATUS_BAD_PAGE);
-#pragma unroll
-        for (int k = 0; k < NLD; ++k) {
-          const uint32_t loff = (uint32_t)(k * RPI + lrow0) * RS + lcol;
-          *reinterpret_cast<vec8*>(kl + loff) = kr[s][k];
-          *reinterpret_cast<vec8*>(vl + loff) = vr[s][k];
-        }
-        wave_lds_sync();
-        if (p == it_start && (cur.flags & kItemLast) && cur.slot >= 0 && lane == 0)
-          b_count = __hip_atomic_load(counters + (int64_t)cur.seq * n_kv_heads + h,
-                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int pn = p + kDepth;
-        if (pn < n_pages) {
-          // halfway through a chunk of 64 page words, fetch the next chunk
-          // into the other register (the chunk it held is long done)
-          if ((pn & 63) == 32 && (pn | 63) + 1 < n_pages) {
-            const int nw = words[(pn | 63) + 1 + lane];
-            if ((pn >> 6) & 1) pw0 = nw; else pw1 = nw;
-          }
-          load_page(pn, kr[s], vr[s]);
-        }
-        compute(p);
-        PKV_TL(if (p == 0) tl_first = __builtin_amdgcn_s_memrealtime();)
-        // (after compute: a merge below uses the wave's tile as scratch)
-        if (pa_state != 0 && p == pa_at) {
-          if (pa_state == 1) {
-            // Page p's loads were issued after the partial's stores and have
-            // arrived; the kDepth - 1 pages and more issued since may still be
-            // outstanding, so this wait leaves the stores complete.
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(OPS * (kDepth - 1)) : "memory");
-            pa_old = arrive(pa_seq);
-            pa_state = 2;
-            pa_at = p + kDepth;
-          } else {
-            finish_arrival();
-          }
-        }
-        if (p == it_end - 1) end_item(p);
-        wave_lds_sync();  // this page's tile reads are done before the next copy
-      }
+    for (int k = 0; k < NLD; ++k) {
+      const uint32_t loff = (uint32_t)(k * RPI + lrow0) * RS + lcol;
+      *reinterpret_cast<vec8*>(kl + loff) = kr[k];
+      *reinterpret_cast<vec8*>(vl + loff) = vr[k];
     }
+    wave_lds_sync();
+    if (p == it_start && (cur.flags & kItemLast) && cur.slot >= 0 && lane == 0)
+      b_count = __hip_atomic_load(counters + (int64_t)cur.seq * n_kv_heads + h,
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wcur = wnext;
+    wnext = words[p + 2];   // inside the plan block: its words are followed by items
+    load_page(p + 1, wcur, kr, vr);
+    compute(p);
+    PKV_TL(if (p == 0) tl_first = __builtin_amdgcn_s_memrealtime();)
+    // (after compute: a merge below uses the wave's tile as scratch)
+    if (pa_state != 0 && p == pa_at) {
+      // Page p's loads were issued after the partial's stores and have
+      // arrived (vmcnt counts in order); only page p + 1's loads may still
+      // be outstanding, so this wait leaves the stores complete.
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(OPS) : "memory");
+      pa_old = arrive(pa_seq);
+      finish_arrival();
+    }
+    if (p == it_end - 1) end_item(p);
+    wave_lds_sync();  // this page's tile reads are done before the next copy
   }
   PKV_TL(const unsigned long long tl_last = __builtin_amdgcn_s_memrealtime();)
   flush_arrival();
@@ -636,8 +658,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
 #endif
 }
 
-static size_t decode_lds_bytes(int hgw, int D) {
-  return (size_t)hgw * (D == 64 ? Tile<_Float16, 64>::BYTES : Tile<_Float16, 128>::BYTES);
+template <typename T, int D, int G>
+static size_t decode_lds_bytes(int hgw) {
+  return (size_t)hgw * (Tile<T, D>::BYTES + Stage<T, D, G>::BYTES);
 }
 
 template <typename T, int D, int G>
@@ -647,8 +670,8 @@ static void launch(const void* q, void* out, void* kp, void* vp, int64_t nb,
                    uint32_t o_bytes, uint32_t ml_bytes, int32_t* cnt, int32_t* status,
                    hipStream_t s) {
   const int hgw = heads_per_wg(Hkv);
-  hipLaunchKernelGGL((decode_kernel<T, D, G>), dim3((unsigned)n_work), dim3(hgw * 64),
-                     decode_lds_bytes(hgw, D), s, (const T*)q, (T*)out, (T*)kp, (T*)vp, nb, plan,
+  const size_t lds = decode_lds_bytes<T, D, G>(hgw);
+  hipLaunchKernelGGL((decode_kernel<T, D, G>), dim3((unsigned)n_work), dim3(hgw * 64), lds, s, (const T*)q, (T*)out, (T*)kp, (T*)vp, nb, plan,
                      stride, Hkv, sl2, (const T*)kn, (const T*)vn, slots, po, pml, o_bytes,
                      ml_bytes, cnt, status);
 }
@@ -659,8 +682,9 @@ template <typename T, int D, int G>
 static int resident(int Hkv) {
   const int hgw = heads_per_wg(Hkv);
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<T, D, G>, hgw * 64,
-                                                   decode_lds_bytes(hgw, D)) != hipSuccess)
+  const size_t lds = decode_lds_bytes<T, D, G>(hgw);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<T, D, G>, hgw * 64, lds) !=
+      hipSuccess)
     return 0;
   return n;
 }
