@@ -48,11 +48,12 @@
 // Cut sequences merge in the same launch. Each piece publishes its partial
 // (o, m, l) with 16-byte buffer stores carrying the sc1 (agent coherence)
 // bit, which write through the per-XCD L2, waits until they have completed
-// (s_waitcnt vmcnt(0)), then bumps its (sequence, head) arrival counter. The
-// wave that sees the last arrival reads the partials back with sc1 loads
-// (never a stale L2 line) and writes the output. This avoids a second launch
-// and an agent-scope release fence, whose L2 write-back walks the whole
-// cache.
+// (s_waitcnt), then bumps its (sequence, head) arrival counter. The wave that
+// sees the last arrival reads the partials back with sc1 loads (never a
+// stale L2 line) and writes the output; a last piece that finds every other
+// piece arrived merges without publishing its own. This avoids a second
+// launch and an agent-scope release fence, whose L2 write-back walks the
+// whole cache.
 //
 // Fused append (optional): when the caller passes the step's new K/V rows,
 // the wave whose piece holds a sequence's last page writes its head's slice
@@ -93,18 +94,25 @@ template <int D, int G> struct PartLayout {
 };
 
 // Split-K merge for one KV head h of sequence seq, run by the wave that
-// published the last partial. Lanes run over partitions for each head row's
-// max M and sum L; then, 64 partitions at a time, the weights 2^(m_s - M)
-// go to this wave's LDS scratch as [partition][GS rows], and the partial
-// outputs are read in the producers' own layout: lane (n, g) takes row group
-// rg = g % NGR of every SPLIT-th partition starting at g / NGR, and the
-// SPLIT lane groups that share a row group are summed by shuffles at the
-// end. The summation order depends only on the partition count, so the
-// result does not depend on the batch.
+// published the last partial, or by the sequence's last piece with its own
+// partial still in registers (`own`). Lanes run over partitions for each
+// head row's max M and sum L; then, 64 partitions at a time, the weights
+// 2^(m_s - M) go to this wave's LDS scratch as [partition][GS rows], and the
+// partial outputs are read in the producers' own layout: lane (n, g) takes
+// row group rg = g % NGR of the chunk's partitions cn - 1 - j for j = g / NGR,
+// g / NGR + SPLIT, ..., and the SPLIT lane groups that share a row group are
+// summed by shuffles at the end. The chunk's last partition goes to lane
+// group 0, whose lanes (n, rg) hold exactly that row group of an own
+// partial in their accumulators, so `own` needs no data movement for o and
+// enters the sums in the same place with the same bits a store and load
+// would give. The summation order depends only on the partition count, so
+// the result does not depend on the batch or on which wave merges.
 template <typename T, int D, int G>
 __device__ __forceinline__ void merge_head(T* __restrict__ out, float* wts, int seq, int h,
                                            int n_kv_heads, int nparts, int slot0,
-                                           __amdgpu_buffer_rsrc_t ro, __amdgpu_buffer_rsrc_t rm) {
+                                           __amdgpu_buffer_rsrc_t ro, __amdgpu_buffer_rsrc_t rm,
+                                           bool own, const f32x4* own_o, float own_m,
+                                           float own_l) {
   typedef PartLayout<D, G> PL;
   constexpr int NDB = D / 16;
   constexpr int NGR = PL::NGR;
@@ -114,32 +122,39 @@ __device__ __forceinline__ void merge_head(T* __restrict__ out, float* wts, int 
   const int n = lane & 15, g = lane >> 4;
   const int rg = g % NGR, so = g / NGR;
   const int Hq = n_kv_heads * G;
+  const int own_part = own ? nparts - 1 : -1;
+  // (m, l) of every head of partitions c0 + lane; an own partition's come
+  // from lanes 0 .. G - 1, which hold head r's running max and sum
   auto load_ml = [&](int c0, float* mr, float* lr) {
-    const bool ok = c0 + lane < nparts;
+    const bool mine = c0 + lane == own_part;
+    const bool ok = c0 + lane < nparts && !mine;
     const uint32_t b2 = (uint32_t)(((int64_t)(slot0 + (ok ? c0 + lane : 0)) * Hq + h * G) * 8);
 #pragma unroll
     for (int r = 0; r < G; ++r) {
       const f32x2 ml =
           __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rm, b2 + 8 * r, 0, kSc1));
-      mr[r] = ok ? ml[0] : -INFINITY;
-      lr[r] = ok ? ml[1] : 0.f;
+      const float m_own = __shfl(own_m, r, 64), l_own = __shfl(own_l, r, 64);
+      mr[r] = ok ? ml[0] : mine ? m_own : -INFINITY;
+      lr[r] = ok ? ml[1] : mine ? l_own : 0.f;
     }
   };
-  // One partition of this lane's stride.
-  auto load_part = [&](int c0, int sl, f32x4* v) {
+  // Partition c0 + cn - 1 - j of this lane's row group (j < cn).
+  auto load_part = [&](int c0, int j, f32x4* v) {
     const int cn = min(64, nparts - c0);
-    const uint32_t off =
-        (uint32_t)(((int64_t)(slot0 + c0 + (sl < cn ? sl : 0)) * n_kv_heads + h) *
-                   PL::FLOATS * 4);
+    const int pi = c0 + cn - 1 - (j < cn ? j : 0);
+    const bool mine = pi == own_part;   // then j == 0: lane group 0
+    const uint32_t off = (uint32_t)(((int64_t)(slot0 + pi) * n_kv_heads + h) * PL::FLOATS * 4);
 #pragma unroll
     for (int b = 0; b < NDB; ++b)
-      v[b] = sl < cn ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           ro, off + ((rg * NDB + b) * 16 + n) * 16, 0, kSc1))
-                     : f32x4{0.f, 0.f, 0.f, 0.f};
+      v[b] = j >= cn ? f32x4{0.f, 0.f, 0.f, 0.f}
+             : mine ? own_o[b]
+                    : __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    ro, off + ((rg * NDB + b) * 16 + n) * 16, 0,
+                                                    kSc1));
   };
-  // The first partition does not depend on the maximum: its loads go out with
-  // the (m, l) loads, so a sequence of up to SPLIT partitions merges in one
-  // round trip.
+  // The first partitions do not depend on the maximum: their loads go out
+  // with the (m, l) loads, so a sequence of up to SPLIT partitions merges in
+  // one round trip.
   f32x4 v[NDB];
   load_part(0, so, v);
   float mr[G], lr[G], M[G], L[G];
@@ -166,9 +181,9 @@ __device__ __forceinline__ void merge_head(T* __restrict__ out, float* wts, int 
     }
     wave_lds_sync();
     const int cn = min(64, nparts - c0);
-    for (int sl = so; sl < cn; sl += SPLIT) {
-      if (c0 > 0 || sl > so) load_part(c0, sl, v);
-      const f32x4 wr = *reinterpret_cast<const f32x4*>(wts + sl * GS + 4 * rg);
+    for (int j = so; j < cn; j += SPLIT) {
+      if (c0 > 0 || j > so) load_part(c0, j, v);
+      const f32x4 wr = *reinterpret_cast<const f32x4*>(wts + (cn - 1 - j) * GS + 4 * rg);
 #pragma unroll
       for (int b = 0; b < NDB; ++b) acc[b] += wr * v[b];
     }
@@ -249,9 +264,11 @@ template <typename T, int D, int G> struct Stage {
 // count it returns is checked at once. The last piece of a
 // cut sequence runs at the end of its bin: it reads the arrival counter when
 // it starts and, if every other piece has arrived by then, merges at its end
-// without counting itself (it publishes its own partial first, so both paths
-// merge the same stored partials in the same order); otherwise it counts
-// its own arrival, and whichever piece arrives last merges.
+// without counting itself, its own partial taken from its registers (the
+// same bits a store and a load would give, in the same place of the
+// summation, so both paths produce the same output) and never stored;
+// otherwise it publishes and counts its own arrival, and whichever piece
+// arrives last merges.
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     const T* __restrict__ q, T* __restrict__ out, T* __restrict__ kpool, T* __restrict__ vpool,
@@ -451,10 +468,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   };
 
   // Merge (seq, h) from the stored partials and reset its counter.
-  auto merge = [&](int sq, int nparts, int slot0) __attribute__((always_inline)) {
+  auto merge = [&](int sq, int nparts, int slot0, bool own) __attribute__((always_inline)) {
     PKV_TL(const unsigned long long tm = __builtin_amdgcn_s_memrealtime(); ++tl_merges;)
     merge_head<T, D, G>(out, reinterpret_cast<float*>(kl), sq, h, n_kv_heads, nparts, slot0,
-                        ro, rm);
+                        ro, rm, own, o, m_run, l_run);
     if (lane == 0)
       __hip_atomic_store(counters + (int64_t)sq * n_kv_heads + h, 0, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
@@ -474,7 +491,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   // check a counted arrival: the last one merges
   auto finish_arrival = [&]() __attribute__((always_inline)) {
     if (__builtin_amdgcn_readfirstlane(pa_old) == pa_nparts - 1)
-      merge(pa_seq, pa_nparts, pa_slot0);
+      merge(pa_seq, pa_nparts, pa_slot0, false);
     pa_state = 0;
   };
   auto flush_arrival = [&]() __attribute__((always_inline)) {  // count a pending arrival now
@@ -492,47 +509,41 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       write_out(cur.seq);
     } else {
       flush_arrival();   // at most one deferred arrival at a time
-      const uint32_t head_off =
-          (uint32_t)(((int64_t)cur.slot * n_kv_heads + h) * PL::FLOATS * 4);
-      if (g < NGR) {
+      const bool last = cur.flags & kItemLast;
+      if (last && __builtin_amdgcn_readfirstlane(b_count) == cur.nparts - 1) {
+        // the sequence's last piece, and every other piece had arrived when
+        // it started: it merges, its own partial straight from registers,
+        // and publishes nothing
+        merge(cur.seq, cur.nparts, cur.slot0, true);
+      } else {
+        const uint32_t head_off =
+            (uint32_t)(((int64_t)cur.slot * n_kv_heads + h) * PL::FLOATS * 4);
+        if (g < NGR) {
 #pragma unroll
-        for (int b = 0; b < NDB; ++b)
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[b]), ro,
-                                                 head_off + ((g * NDB + b) * 16 + n) * 16, 0,
-                                                 kSc1);
-      }
-      if (lane < G)
-        __builtin_amdgcn_raw_buffer_store_b64(
-            __builtin_bit_cast(u32x2, f32x2{m_run, l_run}), rm,
-            (uint32_t)(((int64_t)cur.slot * Hq + h * G + lane) * 8), 0, kSc1);
-      asm volatile("" ::: "memory");  // the stores stay before the loads that follow
-      if (cur.flags & kItemLast) {
-        // the sequence's last piece: merge now if every other piece had
-        // arrived when it started, else count its own arrival
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if (__builtin_amdgcn_readfirstlane(b_count) == cur.nparts - 1) {
-          merge(cur.seq, cur.nparts, cur.slot0);
+          for (int b = 0; b < NDB; ++b)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[b]), ro,
+                                                   head_off + ((g * NDB + b) * 16 + n) * 16, 0,
+                                                   kSc1);
+        }
+        if (lane < G)
+          __builtin_amdgcn_raw_buffer_store_b64(
+              __builtin_bit_cast(u32x2, f32x2{m_run, l_run}), rm,
+              (uint32_t)(((int64_t)cur.slot * Hq + h * G + lane) * 8), 0, kSc1);
+        asm volatile("" ::: "memory");  // the stores stay before the loads that follow
+        pa_seq = cur.seq;
+        pa_nparts = cur.nparts;
+        pa_slot0 = cur.slot0;
+        if (!last && p + 2 < n_pages) {
+          // count it once a page loaded after the stores has arrived
+          pa_state = 1;
+          pa_at = p + 2;
         } else {
-          pa_seq = cur.seq;
-          pa_nparts = cur.nparts;
-          pa_slot0 = cur.slot0;
+          // the last piece with others still out, or the stream ends: count
+          // it now; whichever piece arrives last merges
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
           pa_old = arrive(cur.seq);
           finish_arrival();
         }
-      } else if (p + 2 < n_pages) {
-        // count it once a page loaded after the stores has arrived
-        pa_state = 1;
-        pa_at = p + 2;
-        pa_seq = cur.seq;
-        pa_nparts = cur.nparts;
-        pa_slot0 = cur.slot0;
-      } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        pa_seq = cur.seq;
-        pa_nparts = cur.nparts;
-        pa_slot0 = cur.slot0;
-        pa_old = arrive(cur.seq);
-        finish_arrival();
       }
     }
     ++it_idx;
