@@ -20,12 +20,20 @@ from __future__ import annotations
 
 from dataclasses import dataclass, field
 from itertools import chain
+from operator import attrgetter
 
 import numpy as np
 import torch
 
 from .contract import MIRRORED, BatchMeta, HostMirror, validate_host
 from .paging import SequenceBlocks
+
+_BLOCKS = attrgetter("blocks")
+_NEW_IDS = attrgetter("new_token_ids")
+_NUM_TOKENS = attrgetter("num_tokens")
+_BLOCK_IDS = attrgetter("block_ids")
+_BLOCK_SIZE = attrgetter("block_size")
+_IS_FREED = attrgetter("is_freed")
 
 __all__ = ["ScheduledSeq", "build_batch_meta", "build_token_tensor"]
 
@@ -89,13 +97,15 @@ def build_batch_meta(seqs: list[ScheduledSeq], device, page_size: int,
 
     # Per-sequence scalars in one pass each; the index arrays below are built
     # with array operations from them and the concatenated page lists.
+    # (map over attribute getters: the per-sequence work stays in C)
     n = len(seqs)
-    blocks = [s.blocks for s in seqs]
-    qlens = np.fromiter((len(s.new_token_ids) for s in seqs), np.int64, n)
-    kvlens = np.fromiter((b.num_tokens for b in blocks), np.int64, n)
-    nblk = np.fromiter((len(b.block_ids) for b in blocks), np.int64, n)
-    bsz = np.fromiter((b.block_size for b in blocks), np.int64, n)
-    freed = np.fromiter((b.is_freed for b in blocks), bool, n)
+    blocks = list(map(_BLOCKS, seqs))
+    qlens = np.fromiter(map(len, map(_NEW_IDS, seqs)), np.int64, n)
+    kvlens = np.fromiter(map(_NUM_TOKENS, blocks), np.int64, n)
+    id_lists = list(map(_BLOCK_IDS, blocks))
+    nblk = np.fromiter(map(len, id_lists), np.int64, n)
+    bsz = np.fromiter(map(_BLOCK_SIZE, blocks), np.int64, n)
+    freed = np.fromiter(map(_IS_FREED, blocks), bool, n)
     bad = freed | (qlens <= 0) | (qlens > kvlens) | (kvlens > nblk * bsz) | (bsz != page_size)
     if bad.any():  # the first offender raises the per-sequence message
         i = int(np.argmax(bad))
@@ -112,8 +122,7 @@ def build_batch_meta(seqs: list[ScheduledSeq], device, page_size: int,
     positions = np.arange(T, dtype=np.int64) + (kvlens - qlens - cu[:-1])[batch_idx]
     indptr = np.zeros(n + 1, dtype=np.int64)
     np.cumsum(nblk, out=indptr[1:])
-    indices = np.fromiter(chain.from_iterable(b.block_ids for b in blocks), np.int64,
-                          int(indptr[-1]))
+    indices = np.fromiter(chain.from_iterable(id_lists), np.int64, int(indptr[-1]))
     last = kvlens % page_size
     last[last == 0] = page_size
     # slot = block_ids[p // page_size] * page_size + p % page_size

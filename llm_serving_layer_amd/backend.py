@@ -82,7 +82,13 @@ class _Plan:
 
     __slots__ = ("meta", "use_prefill", "slots", "indptr", "indices", "kv_lens", "cu_q",
                  "bidx", "plan", "n_work", "n_slots", "stride", "n_tokens", "n_seqs", "fusable",
-                 "dec")
+                 "dec", "ptrs")
+
+
+def _decode_ptrs(indptr, indices, kv_lens, plan, slots) -> tuple:
+    """Device addresses a decode launch passes, taken once per plan."""
+    return (indptr.data_ptr(), indices.data_ptr(), kv_lens.data_ptr(), plan.data_ptr(),
+            slots.data_ptr() if slots is not None else None)
 
 
 class _DecodeRows:
@@ -187,14 +193,18 @@ class MI355XBackend:
                                  dtype=dtype, device=self.device)
         self._k_pool = [self._pool[l, 0] for l in range(num_layers)]
         self._v_pool = [self._pool[l, 1] for l in range(num_layers)]
+        # the pools never move: their addresses are taken once
+        self._k_ptr = [t.data_ptr() for t in self._k_pool]
+        self._v_ptr = [t.data_ptr() for t in self._v_pool]
         self._block_bytes = block_size * n_kv_heads * head_dim * self._pool.element_size()
         self._plane_bytes = num_blocks * self._block_bytes
         self._status = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._status_ptr = self._status.data_ptr()
         # The split-K workspace. A pool sized by sizing.plan_kv_pool passes its
         # workspace_bytes here, so no batch within that plan's limits ever
         # allocates at run time; a plan that needs more grows it.
-        self._workspace = torch.zeros(decode_workspace_bytes, dtype=torch.uint8,
-                                      device=self.device)
+        self._set_workspace(torch.zeros(decode_workspace_bytes, dtype=torch.uint8,
+                                        device=self.device))
         self._planned: _Plan | None = None
         self._slot_cache: tuple[BatchMeta, torch.Tensor] | None = None
         self._pending: _Pending | None = None
@@ -249,7 +259,16 @@ class MI355XBackend:
         return t.to(device=self.device, dtype=torch.int32).contiguous()
 
     def _as_pool(self, x: torch.Tensor) -> torch.Tensor:
+        # (a tensor already in the pool dtype, contiguous and on this device is
+        # used as it is, without a conversion call per launch)
+        if x.dtype is self.dtype and x.get_device() == self.device.index and x.is_contiguous():
+            return x
         return x.to(device=self.device, dtype=self.dtype).contiguous()
+
+    def _set_workspace(self, ws: torch.Tensor) -> None:
+        self._workspace = ws
+        self._ws_ptr = ws.data_ptr() if ws.numel() else None
+        self._ws_bytes = ws.numel()
 
     def check_device_errors(self) -> None:
         """
@@ -355,9 +374,9 @@ class MI355XBackend:
 
     def _launch_append(self, layer, k, v, slots, stream) -> None:
         rc = self._lib.pkv_append_kv(
-            self._k_pool[layer].data_ptr(), self._v_pool[layer].data_ptr(),
+            self._k_ptr[layer], self._v_ptr[layer],
             self.num_blocks * self.block_size, k.data_ptr(), v.data_ptr(), slots.data_ptr(),
-            k.shape[0], self.n_kv_heads, self.head_dim, self._code, self._status.data_ptr(),
+            k.shape[0], self.n_kv_heads, self.head_dim, self._code, self._status_ptr,
             stream)
         _native.check(rc, "append_kv")
 
@@ -407,13 +426,12 @@ class MI355XBackend:
             self._flush()
         q = self._as_pool(q)
         out = torch.empty_like(q)
-        kp = self._k_pool[layer_idx].data_ptr()
-        vp = self._v_pool[layer_idx].data_ptr()
+        kp = self._k_ptr[layer_idx]
+        vp = self._v_ptr[layer_idx]
         self.n_runs += 1
         if not p.use_prefill:
-            self._launch_decode(q, out, kp, vp, p.indptr, p.indices, p.kv_lens, p.n_seqs,
-                                p.plan, p.n_work, p.n_slots, p.stride, scale, stream,
-                                pend if fused else None, p.slots)
+            self._launch_decode(q, out, kp, vp, p.ptrs, p.n_seqs, p.n_work, p.n_slots,
+                                p.stride, scale, stream, pend if fused else None)
         else:
             rc = self._lib.pkv_attend_prefill(
                 q.data_ptr(), out.data_ptr(), kp, vp, self.num_blocks, p.cu_q.data_ptr(),
@@ -426,22 +444,22 @@ class MI355XBackend:
             if d is not None:
                 qd = q.index_select(0, d.rows)
                 od = torch.empty_like(qd)
-                self._launch_decode(qd, od, kp, vp, d.indptr, d.indices, d.kv_lens, d.n,
-                                    d.plan, d.n_work, d.n_slots, d.stride, scale, stream, None,
-                                    None)
+                self._launch_decode(qd, od, kp, vp, _decode_ptrs(d.indptr, d.indices,
+                                                                 d.kv_lens, d.plan, None),
+                                    d.n, d.n_work, d.n_slots, d.stride, scale, stream, None)
                 out.index_copy_(0, d.rows, od)
         return out
 
-    def _launch_decode(self, q, out, kp, vp, indptr, indices, kv_lens, n_seqs, plan, n_work,
-                       n_slots, stride, scale, stream, pend, slots) -> None:
-        ws = self._workspace
+    def _launch_decode(self, q, out, kp, vp, ptrs, n_seqs, n_work, n_slots, stride, scale,
+                       stream, pend) -> None:
+        """``ptrs``: device addresses of (indptr, indices, kv_lens, plan, slots)."""
+        indptr, indices, kv_lens, plan, slots = ptrs
         rc = self._lib.pkv_attend_decode(
-            q.data_ptr(), out.data_ptr(), kp, vp, self.num_blocks, indptr.data_ptr(),
-            indices.data_ptr(), kv_lens.data_ptr(), n_seqs, self.n_heads, self.n_kv_heads,
-            self.head_dim, self.block_size, float(scale), self._code, plan.data_ptr(), n_work,
-            n_slots, stride, pend.k.data_ptr() if pend else None,
-            pend.v.data_ptr() if pend else None, slots.data_ptr() if pend else None,
-            ws.data_ptr() if ws.numel() else None, ws.numel(), self._status.data_ptr(), stream)
+            q.data_ptr(), out.data_ptr(), kp, vp, self.num_blocks, indptr, indices, kv_lens,
+            n_seqs, self.n_heads, self.n_kv_heads, self.head_dim, self.block_size,
+            float(scale), self._code, plan, n_work, n_slots, stride,
+            pend.k.data_ptr() if pend else None, pend.v.data_ptr() if pend else None,
+            slots if pend else None, self._ws_ptr, self._ws_bytes, self._status_ptr, stream)
         _native.check(rc, "attend (decode)")
 
     # -- planning ---------------------------------------------------------------
@@ -540,6 +558,7 @@ class MI355XBackend:
         p.bidx = self._dev_i32(meta.batch_indices)
         p.slots = (self._dev_i32(meta.slot_mapping) if meta.slot_mapping is not None
                    else None)
+        p.ptrs = _decode_ptrs(p.indptr, p.indices, p.kv_lens, p.plan, p.slots)
         self._planned = p
         self.n_plans += 1
         return p
@@ -579,7 +598,7 @@ class MI355XBackend:
             part_pages = min(2 * part_pages, MAX_PART_PAGES)
         if need > self._workspace.numel():
             # zero-filled: the arrival counters at the front start at zero
-            self._workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)
+            self._set_workspace(torch.zeros(need, dtype=torch.uint8, device=self.device))
         elif need > 0:
             # a previous layout may have left partial data where counters now sit
             self._workspace[:counter_bytes].zero_()

@@ -829,19 +829,33 @@ extern "C" int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_indic
   typedef std::pair<int64_t, int32_t> Load;  // (work, bin)
   std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
   for (int32_t b = 0; b < bins; ++b) heap.push({0, b});
-  std::vector<std::vector<int32_t>> by_bin((size_t)bins);
+  // (flat arrays: the bin of every item in dealing order, then the items of
+  // each bin gathered by a counting sort, so planning allocates nothing per bin)
+  const size_t n_items = items.size();
+  std::vector<int32_t> bin_of(n_items), bin_count((size_t)bins + 1, 0);
   std::vector<int64_t> bin_pages((size_t)bins, 0);
   for (int32_t ix : order) {
     Load l = heap.top();
     heap.pop();
-    by_bin[l.second].push_back(ix);
+    bin_of[ix] = l.second;
+    ++bin_count[l.second + 1];
     bin_pages[l.second] += items[ix].np;
     heap.push({l.first + items[ix].cost, l.second});
   }
   int64_t stride = kHdrInts;
   for (int64_t b = 0; b < bins; ++b)
     stride = std::max<int64_t>(stride, kHdrInts + ((bin_pages[b] + 3) & ~3LL) +
-                                           kItemInts * (int64_t)by_bin[b].size());
+                                           kItemInts * (int64_t)bin_count[b + 1]);
+  // in a bin: pieces before a cut sequence's last, whole sequences, then last
+  // pieces, each in dealing order (longest first): a stable sort by (bin, role)
+  for (int64_t b = 0; b < bins; ++b) bin_count[b + 1] += bin_count[b];
+  std::vector<int32_t> by_bin(n_items);
+  {
+    std::vector<int32_t> fill(bin_count.begin(), bin_count.end() - 1);
+    for (int role = 0; role < 3; ++role)
+      for (int32_t ix : order)
+        if (items[ix].role == role) by_bin[fill[bin_of[ix]]++] = ix;
+  }
   const int64_t need = bins * stride + kPlanTail;
   if (plan_needed) *plan_needed = need;
   if (stride > 0x7fffffff || need > plan_capacity)
@@ -849,17 +863,13 @@ extern "C" int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_indic
                 (long long)need, (long long)plan_capacity);
   std::fill(plan, plan + need, 0);
   for (int64_t b = 0; b < bins; ++b) {
-    // in a bin: pieces before a cut sequence's last, whole sequences, then
-    // last pieces (each kept in dealing order, longest first)
-    std::stable_sort(by_bin[b].begin(), by_bin[b].end(),
-                     [&](int32_t x, int32_t y) { return items[x].role < items[y].role; });
     int32_t* bp = plan + b * stride;
-    bp[0] = (int32_t)by_bin[b].size();
+    bp[0] = bin_count[b + 1] - bin_count[b];
     bp[1] = (int32_t)bin_pages[b];
     int32_t* w = bp + kHdrInts;
     int32_t* it = w + ((bin_pages[b] + 3) & ~3LL);
-    for (int32_t ix : by_bin[b]) {
-      const Item& x = items[ix];
+    for (int32_t j = bin_count[b]; j < bin_count[b + 1]; ++j) {
+      const Item& x = items[by_bin[j]];
       const int32_t np_seq = kv_indptr[x.seq + 1] - kv_indptr[x.seq];
       for (int32_t t = 0; t < x.np; ++t) {
         const int32_t pg = x.first + t;
