@@ -78,7 +78,7 @@ constexpr int kHdrInts = 4;         // bin header {n_items, n_pages, 0, 0}
 constexpr int kItemInts = 8;        // {seq, n_pages, first token, kv_len, slot, n_pieces,
                                     //  first slot, flags}
 constexpr int kItemLast = 1;        // flags: the piece holds its sequence's last page
-constexpr int kPlanTail = 64;       // zero ints after the last bin (whole-wave word loads)
+constexpr int kPlanTail = 64;       // zero ints after the last bin (words read past its end)
 
 // KV heads per workgroup: one wave each, at most kMaxWaves, dividing Hkv.
 static int heads_per_wg(int hkv) { return hkv % 4 == 0 ? 4 : hkv % 2 == 0 ? 2 : 1; }
