@@ -126,6 +126,56 @@ def test_decode_long_sequences_split_k(part_pages, dtype):
     check(p.step(meta, 3), "split-K", tol, rtol)
 
 
+@pytest.mark.parametrize("geom", [(8, 8, 64), (4, 8, 64), (1, 8, 64), (2, 32, 64),
+                                  (2, 8, 128), (4, 32, 128), (2, 32, 128)])
+def test_split_k_and_packed_items_other_geometries(geom):
+    """Cut sequences and many items per bin at every group size and head_dim
+    the decode kernel instantiates (1 to 16 query heads per KV head, 64 and
+    128 dims): pieces of 3 pages (up to 59 of one sequence), their merges
+    (by the last arriver, or by the last piece with its own partial in
+    registers), and a bin's item slots refilled in batches, with the fused
+    append, over two decode steps against the oracle."""
+    n_kv, n_heads, d = geom
+    print(f"split-K + packed items geom={geom}", flush=True)
+    p = Pair(1, 512, 16, n_kv, n_heads, d, part_pages=3, decode_workgroups=8)
+    p.poison(4)
+    alloc, _keep = fragmented_allocator(512, 16)
+    rng = np.random.default_rng(d * 100 + n_heads)
+    lens = [1, 40, 100, 333, 940] + [int(x) for x in rng.integers(1, 60, 24)]
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(len(lens))]
+    for s, n in zip(seqs, lens):
+        s.append(n)
+    for step in range(2):
+        meta = grow_and_assemble(seqs, [1] * len(lens), 16)
+        check(p.step(meta, 20 + step), f"decode step {step}")
+        plan = p.gpu._planned
+        assert plan.n_slots > 0, "expected cut sequences"
+        assert plan.n_work // (n_kv // min(n_kv, 4)) < len(lens), "expected several items per bin"
+
+
+@pytest.mark.parametrize("geom", [(8, 32, 64), (1, 8, 64), (2, 32, 128)])
+def test_merge_bits_do_not_depend_on_which_wave_merges(geom):
+    """With one bin, every piece of a cut sequence runs before its last piece
+    in the same wave, so the last piece always merges with its own partial
+    from registers; with many bins whichever piece arrives last merges from
+    stored partials. The outputs must be the same bits."""
+    n_kv, n_heads, d = geom
+    print(f"merge paths geom={geom}", flush=True)
+    groups = n_kv // min(n_kv, 4)
+    outs = []
+    for wgs in (groups, 64 * groups):
+        p = Pair(1, 512, 16, n_kv, n_heads, d, part_pages=2, decode_workgroups=wgs)
+        p.poison(6)
+        alloc, _keep = fragmented_allocator(512, 16)
+        seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(6)]
+        for s, n in zip(seqs, [1, 17, 63, 200, 333, 700]):
+            s.append(n)
+        res = p.step(grow_and_assemble(seqs, [1] * 6, 16), 30)
+        check(res, f"workgroups {wgs}")
+        outs.append(res[0][1].cpu())
+    assert torch.equal(outs[0], outs[1])
+
+
 def _shared_prefix_batch(alloc, n_seqs, prefix_tokens):
     """Radix-style sharing: n_seqs tables start with the same prefix blocks
     (refcounted); each then grows its own blocks."""
