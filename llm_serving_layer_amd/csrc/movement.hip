@@ -100,8 +100,19 @@ __global__ __launch_bounds__(256) void block_kernel(
     V* pb = base + plane * plane_vecs + id * block_vecs;
     if (MODE == 1) { src = pb; dst = st; } else { src = st; dst = pb; }
   }
-  for (int64_t c = threadIdx.x; c < block_vecs; c += blockDim.x)
-    __builtin_nontemporal_store(__builtin_nontemporal_load(src + c), dst + c);
+  // Four loads in flight per thread before their stores. The loads are
+  // ordinary (cached): copy-on-write sources repeat (shared prefixes), and a
+  // repeated source is then read from L2. The stores stream (nontemporal).
+  constexpr int U = 4;
+  int64_t c = threadIdx.x;
+  for (; c + (U - 1) * (int64_t)blockDim.x < block_vecs; c += U * (int64_t)blockDim.x) {
+    V t[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) t[u] = src[c + u * blockDim.x];
+#pragma unroll
+    for (int u = 0; u < U; ++u) __builtin_nontemporal_store(t[u], dst + c + u * blockDim.x);
+  }
+  for (; c < block_vecs; c += blockDim.x) __builtin_nontemporal_store(src[c], dst + c);
 }
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
