@@ -34,7 +34,8 @@
 //     beyond G). Lane (head n, group g) then holds the scores of tokens
 //     4g..4g+3 of the page for head n;
 //  2. online softmax in registers: mask past kv_len, running max / sum with
-//     two cross-lane steps; p = 2^(s*scale*log2e - m) rounded to the pool
+//     two row swaps (v_permlane16_swap, v_permlane32_swap: VALU, no LDS
+//     round trip); p = 2^(s*scale*log2e - m) rounded to the pool
 //     dtype -- four values per lane that are exactly the A operand of a
 //     16x16x16 MFMA. The reference max m moves lazily (only when a head's
 //     max grows by more than 2^8), so most pages skip the rescale of o;
@@ -133,7 +134,7 @@ __device__ __forceinline__ void merge_head(T* __restrict__ out, float* wts, int 
     for (int r = 0; r < G; ++r) {
       const f32x2 ml =
           __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rm, b2 + 8 * r, 0, kSc1));
-      const float m_own = __shfl(own_m, r, 64), l_own = __shfl(own_l, r, 64);
+      const float m_own = lane_value(own_m, r), l_own = lane_value(own_l, r);
       mr[r] = ok ? ml[0] : mine ? m_own : -INFINITY;
       lr[r] = ok ? ml[1] : mine ? l_own : 0.f;
     }
@@ -193,8 +194,8 @@ __device__ __forceinline__ void merge_head(T* __restrict__ out, float* wts, int 
   for (int b = 0; b < NDB; ++b) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (SPLIT >= 4) acc[b][i] += __shfl_xor(acc[b][i], 16, 64);
-      if (SPLIT >= 2) acc[b][i] += __shfl_xor(acc[b][i], 32, 64);
+      if (SPLIT >= 4) acc[b][i] = sum_x16(acc[b][i]);
+      if (SPLIT >= 2) acc[b][i] = sum_x32(acc[b][i]);
     }
   }
   if (so == 0) {
@@ -427,12 +428,23 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   const __amdgpu_buffer_rsrc_t ro = ws_rsrc(part_o, o_bytes);
   const __amdgpu_buffer_rsrc_t rm = ws_rsrc(part_ml, ml_bytes);
 
+  // Lane 4 g + i's value of v, in every lane of group g (heads 4 g + i < G;
+  // other groups, whose rows are padding, get 1)
+  auto from_lane = [&](float v, int i) __attribute__((always_inline)) {
+    float x = 1.f;
+#pragma unroll
+    for (int gg = 0; 4 * gg < G; ++gg) {
+      x = g == gg ? lane_value(v, 4 * gg + i) : x;
+    }
+    return x;
+  };
+
   // lane (dim column n, group g) holds heads 4g..4g+3 of dims 16b + n.
   auto write_out = [&](int sq) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * g + i;
-      const float li = __shfl(l_run, r, 64);  // lane r holds head r's sum
+      const float li = from_lane(l_run, i);  // lane r holds head r's sum
       if (r < G) {
 #pragma unroll
         for (int b = 0; b < NDB; ++b)
@@ -578,8 +590,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       sc[i] = tp + 4 * g + i < cur.kv ? acc[i] * scale_log2 : -INFINITY;
       mx = fmaxf(mx, sc[i]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = max_x32(max_x16(mx));
     // Lazy rescale: the reference max moves only when some head's max
     // grows by more than 2^8, so p <= 256 and o / l is unchanged.
     if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f)) {
@@ -590,7 +601,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       // lane (n, g) holds output rows 4g+i, whose factor lives in lane 4g+i
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float a = __shfl(alpha, 4 * g + i, 64);
+        const float a = from_lane(alpha, i);
 #pragma unroll
         for (int b = 0; b < NDB; ++b) o[b][i] *= a;
       }
@@ -603,8 +614,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       ls += e;
       pr[i] = (T)e;
     }
-    ls += __shfl_xor(ls, 16, 64);
-    ls += __shfl_xor(ls, 32, 64);
+    ls = sum_x32(sum_x16(ls));
     l_run += ls;
     const unsigned char* vp = vl + (4 * g + (n >> 2)) * RS + 4 * (n & 3) * (int)sizeof(T);
 #pragma unroll

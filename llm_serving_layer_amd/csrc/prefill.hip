@@ -16,8 +16,8 @@
 //  * S^T = K Q^T: K rows from LDS as the A operand, Q^T held in registers
 //    as the B operand. Lane (row n, group g) gets 16 scores of its query row
 //    n: keys 8 i + 4 g + 0..3, i = 0..3;
-//  * online softmax per query row, lane-local but for one cross-lane step
-//    per max / sum;
+//  * online softmax per query row, lane-local but for one half swap
+//    (v_permlane32_swap) per max / sum;
 //  * O^T = V^T P^T: V^T from transposing LDS reads as the A operand, the
 //    lane's own 8 probabilities of a 16-key block as the B operand (the
 //    contraction index runs over keys 4 g + 0..3, 8 + 4 g + 0..3 of the
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, s[hf][rr]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+    mx = max_x32(mx) * scale_log2;
     // Probabilities against the running reference m_run, taken while the
     // tile's max is still being reduced: 16-key block (hf, qq) of P^T uses
     // the lane's scores rr = 8 qq .. 8 qq + 7 in that order.
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
   // the loads of the tiles past the end land in LDS before the workgroup ends
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run = sum_x32(l_run);
   if (valid) {
     const float inv = 1.f / l_run;
     T* orow = out + ((int64_t)(q0 + qs + tok) * Hq + h * G + r % G) * D + 4 * g;
