@@ -81,11 +81,13 @@ int pkv_append_kv(void* k_pool, void* v_pool, int64_t num_slots,
  * max_workgroups / (n_kv_heads / heads-per-workgroup) bins. The plan is
  * bins blocks of *plan_stride_out ints: {n_items, n_pages, 0, 0}, n_pages
  * page words (kv_indices entries, with the page's live row count - 1 in bits
- * 27..30 and an out-of-range flag in bit 31, padded to a multiple of 4),
- * then n_items items {seq, n_pages, first token, kv_len, partial slot (-1: a
- * whole sequence), pieces of the sequence, its first slot, flags (bit 0: the
- * piece holds the sequence's last page)} -- pieces of cut sequences before
- * their last, whole sequences, then the last pieces; then 64 zero ints.
+ * 27..30 and an out-of-range flag in bit 31), and n_items items {seq,
+ * n_pages, first token, kv_len, partial slot (-1: a whole sequence), pieces
+ * of the sequence, its first slot, flags (bit 0: the piece holds the
+ * sequence's last page)} at the end of the block, item i at 8 (i + 1) ints
+ * before the next block -- pieces of cut sequences before their last, whole
+ * sequences, then the last pieces; then 64 zero ints. *plan_stride_out is at
+ * least 68.
  * *plan_needed (if not NULL) receives the ints required; a plan larger than
  * plan_capacity returns PKV_ERR_CAPACITY and writes nothing else.
  * *n_work_out is the grid size (workgroups), *n_slots_out the partial slots

@@ -79,6 +79,7 @@ constexpr int kHdrInts = 4;         // bin header {n_items, n_pages, 0, 0}
 constexpr int kItemInts = 8;        // {seq, n_pages, first token, kv_len, slot, n_pieces,
                                     //  first slot, flags}
 constexpr int kItemLast = 1;        // flags: the piece holds its sequence's last page
+constexpr int kStageMax = 8;        // items staged in LDS at a time (at most)
 constexpr int kPlanTail = 64;       // zero ints after the last bin (words read past its end)
 
 // KV heads per workgroup: one wave each, at most kMaxWaves, dividing Hkv.
@@ -255,8 +256,13 @@ template <typename T, int D, int G> struct Stage {
 // hg * waves + w through the bin's pages, one piece (item) after another,
 // without restarting the page pipeline at item boundaries. The bin's plan
 // block at plan + bin * stride is {n_items, n_pages, 0, 0}, then n_pages page
-// words (id | (live rows - 1) << 27 | bad << 31, padded to a multiple of 4),
-// then n_items items of kItemInts.
+// words (id | (live rows - 1) << 27 | bad << 31); its n_items items of
+// kItemInts end the block, item i at plan + (bin + 1) * stride - (i + 1) *
+// kItemInts. Header, first words and first items thus all sit at addresses
+// known before any of them is read, so one round trip fetches them all and
+// the first page and Q loads go out after it (the block is at least
+// kHdrInts + kStageMax items long, so the first batch's item reads stay
+// inside it).
 //
 // Cut sequences. A piece that is not its sequence's last publishes its
 // partial (o, m, l) with sc1 stores and goes on streaming; its arrival is
@@ -311,9 +317,34 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   const int g = lane >> 4;   // MFMA k-group
 
   const int32_t* bp = plan + (int64_t)bin * stride;
-  const int n_items = bp[0], n_pages = bp[1];
   const int32_t* words = bp + kHdrInts;
-  const int32_t* items = words + ((n_pages + 3) & ~3);
+  const int32_t* items_end = bp + stride;   // item i: items_end - (i + 1) * kItemInts
+  typedef Stage<T, D, G> SG;
+  static_assert(SG::C <= kStageMax, "the first batch's items lie inside the block");
+  // read together with the header: the first batch's (seq, flags), the
+  // first item and the first two page words
+  int sq0[SG::C], fl0[SG::C];
+#pragma unroll
+  for (int j = 0; j < SG::C; ++j) {
+    sq0[j] = items_end[-(j + 1) * kItemInts];
+    fl0[j] = items_end[-(j + 1) * kItemInts + 7];
+  }
+  struct Item { int seq, np, tok0, kv, slot, nparts, slot0, flags; };
+  auto item_at = [&](int i) __attribute__((always_inline)) -> Item {
+    const int32_t* it = items_end - (int64_t)(i + 1) * kItemInts;
+    return Item{it[0], it[1], it[2], it[3], it[4], it[5], it[6], it[7]};
+  };
+  Item cur = item_at(0);
+  int wcur = words[0];
+  int wnext = words[1];
+  const int n_items = bp[0], n_pages = bp[1];
+  // (keeps every one of these reads ahead of the branch below, so they go
+  // out together instead of after it)
+#pragma unroll
+  for (int j = 0; j < SG::C; ++j) asm volatile("" ::"s"(sq0[j]), "s"(fl0[j]));
+  asm volatile("" ::"s"(cur.seq), "s"(cur.np), "s"(cur.tok0), "s"(cur.kv), "s"(cur.slot),
+               "s"(cur.nparts), "s"(cur.slot0), "s"(cur.flags), "s"(wcur), "s"(wnext), "s"(q),
+               "s"(k_new), "s"(v_new));
   if (n_items <= 0) return;
 
   // This lane's chunk of a page: row k * RPI + lane / CPR, bytes
@@ -340,34 +371,37 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   // SG::C items at a time staged in this wave's LDS slots, loaded in one
   // batch (the first batch before the first pages, so waiting for it never
   // waits for a page).
-  struct Item { int seq, np, tok0, kv, slot, nparts, slot0, flags; };
-  auto item_at = [&](int i) __attribute__((always_inline)) -> Item {
-    const int32_t* it = items + (int64_t)i * kItemInts;
-    return Item{it[0], it[1], it[2], it[3], it[4], it[5], it[6], it[7]};
-  };
   const bool fuse = k_new != nullptr;
-  typedef Stage<T, D, G> SG;
   unsigned char* stg = smem + hgw * TL::BYTES + wave * SG::BYTES;
   // Loads of the slots of items i0 .. i0 + C - 1: lane chunk c = 64 r + lane
   // is 16 bytes w of item i's slot (Q rows of the KV head's G query heads,
   // then the KV head's slice of the new K row and of the new V row).
-  auto stage_load = [&](int i0, u32x4* d) __attribute__((always_inline)) {
+  // (seq, flags) of items i0 .. i0 + C - 1 (the last item repeated past the end)
+  auto stage_fields = [&](int i0, int* sq, int* fl) __attribute__((always_inline)) {
     const int ns = min(SG::C, n_items - i0);
-    int sq[SG::C], fl[SG::C];
 #pragma unroll
     for (int j = 0; j < SG::C; ++j) {
-      const int32_t* it = items + (int64_t)(i0 + min(j, ns - 1)) * kItemInts;
+      const int32_t* it = items_end - (int64_t)(i0 + min(j, ns - 1) + 1) * kItemInts;
       sq[j] = it[0];
       fl[j] = it[7];
     }
+  };
+  auto stage_load = [&](int i0, const int* sq, const int* fl, u32x4* d)
+                        __attribute__((always_inline)) {
+    const int ns = min(SG::C, n_items - i0);
 #pragma unroll
     for (int r = 0; r < SG::ROUNDS; ++r) {
       const int c = r * 64 + lane;
       const int i = c / SG::CPI, w = c - i * SG::CPI;
-      int si = sq[0], fi = fl[0];
+      // item i's fields by masks (a select chain here becomes a lookup
+      // table in scratch memory)
+      int si = 0, fi = 0;
 #pragma unroll
-      for (int j = 1; j < SG::C; ++j)
-        if (i == j) { si = sq[j]; fi = fl[j]; }
+      for (int j = 0; j < SG::C; ++j) {
+        const int msk = -(int)(i == j);
+        si |= sq[j] & msk;
+        fi |= fl[j] & msk;
+      }
       const unsigned char* src = nullptr;
       if (i < ns) {
         if (w < SG::QC)
@@ -389,16 +423,13 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     wave_lds_sync();
   };
   u32x4 sgd[SG::ROUNDS];
-  stage_load(0, sgd);
+  stage_load(0, sq0, fl0, sgd);
   // One page in flight: its registers and its word; the next page's word is
   // read a step ahead.
   vec8 kr[NLD], vr[NLD];
-  int wcur = words[0];
   load_page(0, wcur, kr, vr);
-  int wnext = words[1];
   stage_store(sgd);
 
-  Item cur = item_at(0);
   vec8 qb[NCH], kx{}, vx{};
   int new_slot = 0;
   // Item i (slot i % C staged) becomes current: Q^T as the QK B operand
@@ -561,7 +592,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     ++it_idx;
     if (it_idx < n_items) {
       if (it_idx % SG::C == 0) {   // the next batch of slots
-        stage_load(it_idx, sgd);
+        int sq[SG::C], fl[SG::C];
+        stage_fields(it_idx, sq, fl);
+        stage_load(it_idx, sq, fl, sgd);
         stage_store(sgd);
       }
       cur = item_at(it_idx);
@@ -852,7 +885,7 @@ extern "C" int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_indic
     bin_pages[l.second] += items[ix].np;
     heap.push({l.first + items[ix].cost, l.second});
   }
-  int64_t stride = kHdrInts;
+  int64_t stride = kHdrInts + kStageMax * kItemInts;
   for (int64_t b = 0; b < bins; ++b)
     stride = std::max<int64_t>(stride, kHdrInts + ((bin_pages[b] + 3) & ~3LL) +
                                            kItemInts * (int64_t)bin_count[b + 1]);
@@ -877,8 +910,8 @@ extern "C" int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_indic
     bp[0] = bin_count[b + 1] - bin_count[b];
     bp[1] = (int32_t)bin_pages[b];
     int32_t* w = bp + kHdrInts;
-    int32_t* it = w + ((bin_pages[b] + 3) & ~3LL);
     for (int32_t j = bin_count[b]; j < bin_count[b + 1]; ++j) {
+      int32_t* it = bp + stride - (int64_t)(j - bin_count[b] + 1) * kItemInts;
       const Item& x = items[by_bin[j]];
       const int32_t np_seq = kv_indptr[x.seq + 1] - kv_indptr[x.seq];
       for (int32_t t = 0; t < x.np; ++t) {
@@ -951,7 +984,7 @@ static int attend_decode(const void* q, void* out, void* k_pool, void* v_pool,
                           n_seqs, n_heads, n_kv_heads, head_dim, page_size, scale, dtype,
                           status_word, s);
   }
-  if (!plan || n_work <= 0 || n_slots < 0 || plan_stride < kHdrInts)
+  if (!plan || n_work <= 0 || n_slots < 0 || plan_stride < kHdrInts + kStageMax * kItemInts)
     return fail(PKV_ERR_INVALID, "decode needs a plan (pkv_plan_decode)");
   if (n_work % (n_kv_heads / heads_per_wg(n_kv_heads)))
     return fail(PKV_ERR_INVALID, "n_work=%d is not a whole number of bins", n_work);

@@ -151,11 +151,11 @@ def plan_decode(kv_lens, part_pages, workgroups=512, n_kv_heads=8, ps=16, indice
         blk = buf[b * S:(b + 1) * S]
         n_items, n_pg = int(blk[0]), int(blk[1])
         words = blk[4:4 + n_pg].astype(np.int64) & 0xFFFFFFFF
-        base = 4 + ((n_pg + 3) & ~3)
+        assert 4 + n_pg <= S - 8 * n_items, "words and items overlap"
         items, pos = [], 0
-        for i in range(n_items):
+        for i in range(n_items):   # item i ends the block, 8 ints from its end per item
             seq, np_, tok0, kv, slot, nparts, slot0, flags = (int(x) for x in
-                                                              blk[base + 8 * i:base + 8 * i + 8])
+                                                              blk[S - 8 * (i + 1):S - 8 * i])
             pages = [(int(w & ((1 << 27) - 1)), int((w >> 27) & 15) + 1, bool(w >> 31))
                      for w in words[pos:pos + np_]]
             pos += np_

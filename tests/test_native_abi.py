@@ -282,8 +282,7 @@ def test_mixed_batch_plans_its_decodes_for_the_decode_kernel():
     seqs_planned = set()
     for b in range(d.n_work // 2):
         blk = d.plan[b * d.stride:(b + 1) * d.stride].numpy()
-        base = 4 + ((int(blk[1]) + 3) & ~3)
-        seqs_planned |= {int(blk[base + 8 * i]) for i in range(int(blk[0]))}
+        seqs_planned |= {int(blk[d.stride - 8 * (i + 1)]) for i in range(int(blk[0]))}
     assert d.n_slots > 0 and seqs_planned == {0, 1}, "decode plan over the sub-batch"
 
 
