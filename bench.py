@@ -535,8 +535,8 @@ def bench_timeline(args):
         ("one paged decode launch of the batch-256 headline step (lognormal mean 258), "
          f"{GEOM}"),
         batch=256, pages=pages, part_pages=args.part_pages)
-    # wave w of the grid: workgroup w // waves (dispatched round-robin over
-    # the 8 XCDs), KV head group (workgroup % groups), head in the group w % waves
+    # record w: wave w % waves of workgroup w // waves = bin * groups + KV
+    # head group, its dispatch index (round-robin over the 8 XCDs)
     hgw = 4 if HKV % 4 == 0 else 2 if HKV % 2 == 0 else 1
     head = (wid // hgw % (HKV // hgw)) * hgw + wid % hgw
     xcd = (wid // hgw) % 8
