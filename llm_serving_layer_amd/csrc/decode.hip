@@ -869,6 +869,18 @@ extern "C" int pkv_plan_decode(const int32_t* kv_indptr, const int32_t* kv_indic
   const int n_groups = n_kv_heads / hgw;
   int64_t bins = std::max<int64_t>(1, max_workgroups / n_groups);
   bins = std::min<int64_t>(bins, (int64_t)items.size());
+  // A cut piece at least half a bin long usually ends its bin, so the
+  // publish / count / merge chain after its last page adds to that bin's
+  // time instead of overlapping the next piece's pages: it is charged 72
+  // (4.5 pages) instead of the last piece's 40 (measured on the batch-256
+  // decode step: 1.4% faster; no change where bins hold many pieces).
+  {
+    int64_t total = 0;
+    for (const Item& x : items) total += (int64_t)x.np * 16;
+    const int64_t half_bin = total / bins / 2;
+    for (Item& x : items)
+      if (x.role != 1 && (int64_t)x.np * 16 >= half_bin) x.cost = (int64_t)x.np * 16 + 4 + 72;
+  }
   // longest-processing-time-first deal into the least-loaded bin
   std::vector<int32_t> order(items.size());
   for (size_t i = 0; i < order.size(); ++i) order[i] = (int32_t)i;
