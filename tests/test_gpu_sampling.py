@@ -38,7 +38,7 @@ def test_greedy_equals_torch_argmax(dtype, rows, vocab):
         assert got.tolist() == greedy_ids(x.float().cpu().numpy())
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_greedy_ties_nan_and_infinities(dtype):
     print(f"greedy special rows {dtype}", flush=True)
     vocab = 5000
@@ -56,6 +56,26 @@ def test_greedy_ties_nan_and_infinities(dtype):
     assert got.tolist() == greedy_ids(x.float().cpu().numpy())
     assert torch.equal(got, torch.argmax(x, dim=-1))
     assert got.tolist()[:6] == [17, 0, 2500, 9, 0, 4999]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_greedy_single_max_or_nan_at_every_position(dtype):
+    """One row per position p of the first 80 (every element of several
+    16-byte chunks): the row's only maximum at p, a runner-up 40 further on;
+    then the same rows with a NaN at p instead, and a NaN at p after a
+    larger NaN-free maximum. Rows are 16-byte aligned (vocab 4096)."""
+    print(f"greedy every position {dtype}", flush=True)
+    vocab, n = 4096, 80
+    x = torch.zeros(n, vocab, device=DEV, dtype=dtype)
+    idx = torch.arange(n, device=DEV)
+    x[idx, idx] = 5
+    x[idx, idx + 40] = 3
+    assert greedy(x).tolist() == list(range(n))
+    y = torch.zeros(n, vocab, device=DEV, dtype=dtype)
+    y[idx, idx] = math.nan
+    y[idx, (idx + 7) % n] = 9
+    assert greedy(y).tolist() == list(range(n))
+    assert torch.equal(greedy(y), torch.argmax(y, dim=-1))
 
 
 def test_greedy_strided_and_unaligned_rows():
