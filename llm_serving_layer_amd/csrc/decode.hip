@@ -208,9 +208,10 @@ __device__ __forceinline__ void merge_head(T* __restrict__ out, float* wts, int 
       for (int rr = 1; rr < G; ++rr)  // static indices keep L in registers
         if (r == rr) lr_ = L[rr];
       if (r < G) {
+        const float inv = 1.f / lr_;   // one division per row, not per element
 #pragma unroll
         for (int b = 0; b < NDB; ++b)
-          out[((int64_t)seq * Hq + h * G + r) * D + 16 * b + n] = (T)(acc[b][i] / lr_);
+          out[((int64_t)seq * Hq + h * G + r) * D + 16 * b + n] = (T)(acc[b][i] * inv);
       }
     }
   }
@@ -480,9 +481,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       const int r = 4 * g + i;
       const float li = from_lane(l_run, i);  // lane r holds head r's sum
       if (r < G) {
+        const float inv = 1.f / li;   // one division per row, not per element
 #pragma unroll
         for (int b = 0; b < NDB; ++b)
-          out[((int64_t)sq * Hq + h * G + r) * D + 16 * b + n] = (T)(o[b][i] / li);
+          out[((int64_t)sq * Hq + h * G + r) * D + 16 * b + n] = (T)(o[b][i] * inv);
       }
     }
   };
