@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from llm_serving_layer_amd import BlockAllocator, SequenceBlocks
-from llm_serving_layer_amd.backend import MI355XBackend
+from llm_serving_layer_amd.backend import DEFAULT_PART_PAGES, MI355XBackend
 from oracle import PagedTorchOracle
 
 from ._util import (assert_attention_close, fragmented_allocator, grow_and_assemble,
@@ -305,13 +305,16 @@ def test_config1_fp16_fast_path_and_fp32_fixture():
             assert_attention_close(out, want, label="config1 fp16")
 
 
-def test_config2_batch256_one_layer_vs_oracle():
-    """Full decode-bench batch (256 sequences, lognormal mean 258) on one layer."""
-    print("config2 batch 256 parity", flush=True)
+@pytest.mark.parametrize("part_pages", [4, DEFAULT_PART_PAGES])
+def test_config2_batch256_one_layer_vs_oracle(part_pages):
+    """Full decode-bench batch (256 sequences, lognormal mean 258), fused
+    append then attend on two layers, at 4-page partitions and at the
+    backend's default (the headline's setting)."""
+    print(f"config2 batch 256 parity part_pages={part_pages}", flush=True)
     lens = lognormal_lengths(256, 256, 0.8, 2048, 20260731)
     pages = sum(-(-(n + 1) // 16) for n in lens)
     nb = 2 * pages
-    p = Pair(2, nb, 16, 8, 32, 64)
+    p = Pair(2, nb, 16, 8, 32, 64, part_pages=part_pages)
     g = torch.Generator().manual_seed(5)
     perm = torch.randperm(nb, generator=g).tolist()
     a = BlockAllocator(nb, 16)
