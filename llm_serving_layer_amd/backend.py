@@ -331,22 +331,29 @@ class MI355XBackend:
     def append_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor,
                   meta: BatchMeta) -> None:
         """Scatter this step's K/V into the pool through ``meta.slot_mapping``."""
-        self._check_layer(layer_idx)
+        # (checks and conversions inlined: this runs once per layer per step)
+        if layer_idx is None or not 0 <= layer_idx < self.num_layers:
+            self._check_layer(layer_idx)
         if meta.slot_mapping is None:
             raise ValueError("MI355XBackend.append_kv requires meta.slot_mapping")
-        tokens = k.shape[0]
-        if tuple(k.shape) != (tokens, self.n_kv_heads, self.head_dim):
-            raise ValueError(f"k has shape {tuple(k.shape)}, expected "
+        ks = k.shape
+        tokens = ks[0]
+        if ks != (tokens, self.n_kv_heads, self.head_dim):
+            raise ValueError(f"k has shape {tuple(ks)}, expected "
                              f"({tokens}, {self.n_kv_heads}, {self.head_dim})")
-        if v.shape != k.shape:
-            raise ValueError(f"v shape {tuple(v.shape)} != k shape {tuple(k.shape)}")
+        if v.shape != ks:
+            raise ValueError(f"v shape {tuple(v.shape)} != k shape {tuple(ks)}")
         if meta.slot_mapping.shape[0] != tokens:
             raise ValueError(f"slot_mapping has {meta.slot_mapping.shape[0]} entries but "
                              f"{tokens} tokens were supplied")
-        self._flush()
-        k = self._as_pool(k)
-        v = self._as_pool(v)
-        stream = _current_stream(self.device)
+        if self._pending is not None:
+            self._flush()
+        dt, di = self.dtype, self.device.index
+        if not (k.dtype is dt and k.get_device() == di and k.is_contiguous()):
+            k = self._as_pool(k)
+        if not (v.dtype is dt and v.get_device() == di and v.is_contiguous()):
+            v = self._as_pool(v)
+        stream = _raw_stream(di) if _raw_stream is not None else _current_stream(self.device)
         if self._fuse_append:
             try:
                 p = self._ensure_planned(meta)
@@ -407,24 +414,30 @@ class MI355XBackend:
     def attend(self, q: torch.Tensor, layer_idx: int, scale: float,
                meta: BatchMeta) -> torch.Tensor:
         """Causal GQA attention over each sequence's full paged history."""
-        self._check_layer(layer_idx)
-        tokens = q.shape[0]
-        if tuple(q.shape) != (tokens, self.n_heads, self.head_dim):
-            raise ValueError(f"q has shape {tuple(q.shape)}, expected "
+        if layer_idx is None or not 0 <= layer_idx < self.num_layers:
+            self._check_layer(layer_idx)
+        qs = q.shape
+        tokens = qs[0]
+        if qs != (tokens, self.n_heads, self.head_dim):
+            raise ValueError(f"q has shape {tuple(qs)}, expected "
                              f"({tokens}, {self.n_heads}, {self.head_dim})")
         if meta.n_tokens != tokens:
             raise ValueError(f"meta describes {meta.n_tokens} tokens but q has {tokens}")
-        p = self._ensure_planned(meta)
-        stream = _current_stream(self.device)
+        p = self._planned
+        if p is None or p.meta is not meta:
+            p = self._ensure_planned(meta)
+        di = self.device.index
+        stream = _raw_stream(di) if _raw_stream is not None else _current_stream(self.device)
         pend = self._pending
         fused = (pend is not None and pend.layer == layer_idx and pend.meta is meta
                  and pend.stream == stream and p.fusable)
         if fused:
             self._check_pending_intact(pend)
             self._pending = None
-        else:
+        elif pend is not None:
             self._flush()
-        q = self._as_pool(q)
+        if not (q.dtype is self.dtype and q.get_device() == di and q.is_contiguous()):
+            q = self._as_pool(q)
         out = torch.empty_like(q)
         kp = self._k_ptr[layer_idx]
         vp = self._v_ptr[layer_idx]
