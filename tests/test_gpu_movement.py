@@ -114,6 +114,39 @@ def test_copy_blocks_every_layer_bit_exact(dtype):
     bk.check_device_errors()
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_copy_blocks_random_bit_exact(seed):
+    """Seeded random pools (KV heads, head_dim, block size, layers, dtype)
+    and random copy-on-write batches: distinct destinations, sources drawn
+    with repeats (a shared prefix copied to several sequences), against the
+    closed form."""
+    import random
+    r = random.Random(seed)
+    n_kv, d = r.choice([(8, 64), (2, 128), (1, 8), (4, 32)])
+    bs, layers = r.choice([1, 4, 16]), r.randint(1, 5)
+    nb = r.randint(8, 96)
+    dtype = r.choice([torch.float16, torch.bfloat16, torch.float32])
+    print(f"copy_blocks random seed={seed} kv={n_kv} d={d} bs={bs} L={layers} nb={nb} {dtype}",
+          flush=True)
+    bk = backend(num_layers=layers, num_blocks=nb, block_size=bs, n_kv=n_kv,
+                 n_heads=n_kv, head_dim=d, dtype=dtype)
+    poison(bk, 100 + seed)
+    n = r.randint(1, nb // 2)
+    dsts = r.sample(range(nb), n)
+    pool = [b for b in range(nb) if b not in dsts]
+    shared = r.sample(pool, max(1, len(pool) // 8))
+    srcs = [r.choice(shared) if r.random() < 0.27 else r.choice(pool) for _ in range(n)]
+    pairs = list(zip(srcs, dsts))
+    want_k, want_v = copy_blocks_closed_form([p.float().cpu().numpy() for p in bk.k_pool],
+                                             [p.float().cpu().numpy() for p in bk.v_pool], pairs)
+    bk.copy_blocks(srcs, dsts)
+    torch.cuda.synchronize()
+    for layer in range(layers):
+        assert np.array_equal(bk.k_pool[layer].float().cpu().numpy(), want_k[layer])
+        assert np.array_equal(bk.v_pool[layer].float().cpu().numpy(), want_v[layer])
+    bk.check_device_errors()
+
+
 def test_copy_block_contract():
     print("copy_block single pair / errors", flush=True)
     bk = backend(num_layers=3, num_blocks=8, block_size=4, n_kv=2, n_heads=4, head_dim=8,
