@@ -779,7 +779,14 @@ def bench_swap(args):
 
     log(f"swap: {n_seq} x {toks} tokens, {nbytes / 2**20:.0f} MiB each way")
     outs, ins = [], []
-    for it in range(args.warmup + args.steps):
+    n_iter = args.warmup + args.steps
+    for it in range(n_iter):
+        if it == n_iter - 1:
+            # outside the timed region: every victim's bytes before the last
+            # round trip, (2, L, blocks, bs, Hkv, d) in logical block order
+            torch.cuda.synchronize()
+            before = [bk._pool[:, :, torch.tensor(s.block_ids, device=device)]
+                      .transpose(0, 1).cpu() for s in seqs]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         handles = [space.swap_out(f"r{i}", s) for i, s in enumerate(seqs)]
@@ -797,6 +804,15 @@ def bench_swap(args):
             space.swap_in(h, s)
         torch.cuda.synchronize()
         t3 = time.perf_counter()
+        if it == n_iter - 1:
+            # outside the timed region: the host copies equal the victims'
+            # blocks as they were, and the blocks they were restored into
+            # hold the same bytes (raises on a mismatch)
+            for i, (h, s) in enumerate(zip(handles, fresh)):
+                back = bk._pool[:, :, torch.tensor(s.block_ids, device=device)]
+                if not (torch.equal(h.host_buffer, before[i])
+                        and torch.equal(back.transpose(0, 1).cpu(), before[i])):
+                    raise RuntimeError(f"swap round trip of sequence {i} is not bit-exact")
         for h in handles:
             space.release(h)
         seqs = fresh
@@ -821,6 +837,8 @@ def bench_swap(args):
                      "peak_source": "pinned copy of the same size in this run",
                      "link_d2h_GB/s": round(link["d2h"], 2),
                      "link_h2d_GB/s": round(link["h2d"], 2)},
+        "parity": "last round trip bit-exact: every handle's host bytes and every restored "
+                  "block equal the victim's blocks before swap-out",
     })
     return line
 

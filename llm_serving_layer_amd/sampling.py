@@ -28,6 +28,20 @@ from .backend import _DTYPES, _current_stream
 __all__ = ["greedy", "StepTimer", "greedy_step"]
 
 
+def rows_for_kernel(logits: torch.Tensor) -> torch.Tensor:
+    """
+    ``logits`` itself when the argmax kernel can read it in place -- unit
+    element stride and rows that do not overlap (row stride >= vocab, or a
+    single row) -- else a contiguous copy. A view whose rows overlap (an
+    ``expand`` has row stride 0) would otherwise make the kernel read rows
+    1..n-1 past the end of the allocation.
+    """
+    n, vocab = logits.shape
+    unit = logits.stride(1) == 1 or vocab == 1
+    apart = n <= 1 or logits.stride(0) >= vocab
+    return logits if unit and apart else logits.contiguous()
+
+
 def greedy(logits: torch.Tensor) -> torch.Tensor:
     """
     ``torch.argmax(logits, dim=-1)`` for a (n_rows, vocab) f16, bf16 or f32
@@ -44,13 +58,14 @@ def greedy(logits: torch.Tensor) -> torch.Tensor:
     n, vocab = logits.shape
     if vocab == 0:
         raise ValueError("argmax of an empty row: vocab is 0")
-    if logits.stride(1) != 1 and vocab > 1:
-        logits = logits.contiguous()
+    logits = rows_for_kernel(logits)
     out = torch.empty(n, dtype=torch.int64, device=logits.device)
     if n == 0:
         return out
     lib = _native.load()
-    rc = lib.pkv_argmax_rows(logits.data_ptr(), n, vocab, max(logits.stride(0), vocab),
+    # (one row: its stride is never used, and may be anything, e.g. 0)
+    row_stride = logits.stride(0) if n > 1 else vocab
+    rc = lib.pkv_argmax_rows(logits.data_ptr(), n, vocab, row_stride,
                              _DTYPES[logits.dtype], out.data_ptr(),
                              _current_stream(logits.device))
     _native.check(rc, "greedy argmax")

@@ -292,6 +292,11 @@ class KVPoolPlan:
 
         if dtype is None:
             dtype = {2: torch.float16, 4: torch.float32}[self.shape.dtype_bytes]
+        # the decode workspace this plan reserved, and the partition size it
+        # was reserved for: a batch within the plan's limits then never
+        # allocates while a step runs
+        kwargs.setdefault("decode_workspace_bytes", self.workspace_bytes)
+        kwargs.setdefault("part_pages", self.part_pages)
         return MI355XBackend(self.shape.n_layers, self.num_blocks, self.block_size,
                              self.shape.n_kv_heads, n_heads or self.n_heads, self.shape.head_dim,
                              device=device, dtype=dtype, **kwargs)
@@ -337,7 +342,7 @@ def plan_kv_pool(total_vram_bytes: int | None = MI355X_HBM_BYTES,
         raise SizingError(
             f"Model weights ({model_weight_bytes:,} B, {model_weight_bytes / GIB:.2f} GiB) "
             f"exceed total VRAM ({total_vram_bytes:,} B, {total_vram_bytes / GIB:.2f} GiB). "
-            "The model does not fit; there is no KV pool to size.")
+            "Nothing is left over for KV blocks once the weights are loaded.")
     available = total_vram_bytes - model_weight_bytes - activation_headroom_bytes
     if available <= 0:
         raise SizingError(
@@ -367,7 +372,7 @@ def plan_kv_pool(total_vram_bytes: int | None = MI355X_HBM_BYTES,
         raise SizingError(
             f"Available KV memory ({available:,} B) is smaller than one block "
             f"({per_block:,} B at block_size={block_size}) plus its decode workspace. "
-            "A zero-block pool cannot serve a single token.")
+            "The pool would hold no block at all, so not even one token could be cached.")
     ws = workspace(n)
     used = n * per_block
     return KVPoolPlan(shape=shape, total_vram_bytes=int(total_vram_bytes),

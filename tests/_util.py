@@ -164,3 +164,28 @@ def plan_decode(kv_lens, part_pages, workgroups=512, n_kv_heads=8, ps=16, indice
         assert pos == n_pg
         bins.append(items)
     return indptr, bins, nw.value, ns.value
+
+
+def meta_to_device(meta: BatchMeta, device, mirror: bool = True) -> BatchMeta:
+    """
+    ``meta`` with every tensor field moved to ``device``. With ``mirror``
+    (the default) the result carries a host mirror of its index fields,
+    built from ``meta``'s own values, exactly as ``build_batch_meta(...,
+    device=...)`` leaves one: the backend then plans from the host arrays, as
+    a serving loop does. With ``mirror=False`` it has none, and the backend
+    reads the device tensors back to plan.
+    """
+    import dataclasses
+
+    from llm_serving_layer_amd.contract import MIRRORED, HostMirror
+
+    moved = {f.name: getattr(meta, f.name).to(device) for f in dataclasses.fields(meta)
+             if isinstance(getattr(meta, f.name), torch.Tensor)}
+    host = None
+    if mirror:
+        arrays = {k: (None if getattr(meta, k) is None
+                      else getattr(meta, k).cpu().numpy().astype(np.int64)) for k in MIRRORED}
+        host = HostMirror(arrays=arrays, of=tuple(moved.get(k) for k in MIRRORED))
+    out = dataclasses.replace(meta, **moved, host=host)
+    assert (out.host_arrays() is not None) == mirror
+    return out

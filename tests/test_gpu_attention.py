@@ -24,7 +24,7 @@ from llm_serving_layer_amd.backend import DEFAULT_PART_PAGES, MI355XBackend
 from oracle import PagedTorchOracle
 
 from ._util import (assert_attention_close, fragmented_allocator, grow_and_assemble,
-                    lognormal_lengths, make_meta)
+                    lognormal_lengths, make_meta, meta_to_device)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -53,10 +53,10 @@ class Pair:
     def rand(self, shape, g, scale=1.0):
         return (torch.randn(shape, generator=g) * scale).to(self.dtype)
 
-    def step(self, meta_cpu, seed, scale=0.125, layers=None, kv_scale=1.0):
+    def step(self, meta_cpu, seed, scale=0.125, layers=None, kv_scale=1.0, mirror=True):
         """append + attend for each layer; returns [(layer, gpu_out, ref_out)]."""
         g = torch.Generator().manual_seed(seed)
-        meta_gpu = _to_dev(meta_cpu)
+        meta_gpu = _to_dev(meta_cpu, mirror)
         T = meta_cpu.n_tokens
         res = []
         for layer in (layers if layers is not None else range(self.gpu.num_layers)):
@@ -72,10 +72,10 @@ class Pair:
         return res
 
 
-def _to_dev(meta):
-    return dataclasses.replace(meta, **{f.name: getattr(meta, f.name).to(DEV)
-                                        for f in dataclasses.fields(meta)
-                                        if isinstance(getattr(meta, f.name), torch.Tensor)})
+def _to_dev(meta, mirror=True):
+    """On the device, with the host mirror a serving loop's meta carries
+    (the backend plans from it), unless ``mirror=False``."""
+    return meta_to_device(meta, DEV, mirror)
 
 
 def check(res, label, atol=2e-3, rtol=1e-2):
@@ -305,12 +305,15 @@ def test_config1_fp16_fast_path_and_fp32_fixture():
             assert_attention_close(out, want, label="config1 fp16")
 
 
-@pytest.mark.parametrize("part_pages", [4, DEFAULT_PART_PAGES])
-def test_config2_batch256_one_layer_vs_oracle(part_pages):
+@pytest.mark.parametrize("part_pages, mirror", [(4, True), (DEFAULT_PART_PAGES, True),
+                                                (DEFAULT_PART_PAGES, False)])
+def test_config2_batch256_one_layer_vs_oracle(part_pages, mirror):
     """Full decode-bench batch (256 sequences, lognormal mean 258), fused
     append then attend on two layers, at 4-page partitions and at the
-    backend's default (the headline's setting)."""
-    print(f"config2 batch 256 parity part_pages={part_pages}", flush=True)
+    backend's default (the headline's setting); planned from the host
+    mirror a serving loop's meta carries, and (``mirror=False``) from the
+    device tensors read back."""
+    print(f"config2 batch 256 parity part_pages={part_pages} mirror={mirror}", flush=True)
     lens = lognormal_lengths(256, 256, 0.8, 2048, 20260731)
     pages = sum(-(-(n + 1) // 16) for n in lens)
     nb = 2 * pages
@@ -330,7 +333,7 @@ def test_config2_batch256_one_layer_vs_oracle(part_pages):
         p.gpu.append_kv(layer, k.to(DEV), v.to(DEV), _to_dev(hist))
         p.ref.append_kv(layer, k.float(), v.float(), hist)
     meta = grow_and_assemble(seqs, [1] * 256, 16)
-    check(p.step(meta, 8, kv_scale=0.5), "config2")
+    check(p.step(meta, 8, kv_scale=0.5, mirror=mirror), "config2")
 
 
 # ------------------------------------------------------ known answers

@@ -285,3 +285,64 @@ def test_swap_bulk_bit_exact():
     for l in range(16):
         assert np.array_equal(after[l, 0], exp_k[l]) and np.array_equal(after[l, 1], exp_v[l]), l
     swap.release(h)
+
+
+def test_swap_64_victims_lifo_one_handle_each():
+    """The preemption workload the way the reference's scheduler swaps
+    (serving/scheduler/preemption.py:399-472; LIFO victims, :130-194): 64
+    running sequences of 256 tokens (16 blocks each) on a shuffled 16-layer
+    pool are swapped out one handle per victim, the most recently admitted
+    first. Each victim's blocks are freed as soon as its swap_out returns
+    and overwritten at once on the caller's stream (another owner taking
+    them), while that victim's and earlier victims' transfers are still in
+    flight. Then every victim is swapped back into new blocks. Each handle's
+    host bytes must equal the logical-order gather of the pool as it was
+    before the swaps, and the pool after all swap-ins the scatter of every
+    handle into its new blocks over the overwritten pool."""
+    print("swap 64 victims x 16 blocks, LIFO, one handle each", flush=True)
+    L, n_vict, per = 16, 64, 16
+    nb = 2 * n_vict * per + 256
+    bk = backend(num_layers=L, num_blocks=nb, dtype=torch.float16)
+    poison(bk, 13)
+    a = BlockAllocator(nb, 16)
+    a.allocate(nb)
+    a.free(torch.randperm(nb, generator=torch.Generator().manual_seed(14)).tolist())
+    victims = [SequenceBlocks(a, seq_id=i) for i in range(n_vict)]
+    for s in victims:
+        s.append(per * 16)
+    torch.cuda.synchronize()
+    before = bk._pool.cpu().numpy()                      # (L, 2, NB, bs, Hkv, d)
+    swap = KVSwapSpace(bk)
+    handles = []
+    for s in reversed(victims):                          # LIFO: last admitted first
+        old = list(s.block_ids)
+        h = swap.swap_out(f"req-{s.seq_id}", s)
+        s.free()
+        # the freed blocks are rewritten right away on the caller's stream
+        ids = torch.tensor(old, dtype=torch.int64, device=DEV)
+        bk._pool.index_fill_(2, ids, float(s.seq_id % 7) - 3.0)
+        handles.append((s.seq_id, h, old))
+    assert swap.num_swapped == n_vict
+    for sid, h, old in handles:                          # each waits for its own copy only
+        want_k = gather_closed_form([before[l, 0] for l in range(L)], old)
+        want_v = gather_closed_form([before[l, 1] for l in range(L)], old)
+        assert np.array_equal(h.k.numpy(), want_k), f"victim {sid} K"
+        assert np.array_equal(h.v.numpy(), want_v), f"victim {sid} V"
+    torch.cuda.synchronize()
+    mid = bk._pool.cpu().numpy()
+    exp_k = [mid[l, 0] for l in range(L)]
+    exp_v = [mid[l, 1] for l in range(L)]
+    for sid, h, old in reversed(handles):                # resume in admission order
+        new = SequenceBlocks(a, seq_id=1000 + sid)
+        new.append(per * 16)
+        assert new.block_ids != old
+        swap.swap_in(h, new)
+        exp_k = scatter_closed_form(exp_k, h.k.numpy(), new.block_ids)
+        exp_v = scatter_closed_form(exp_v, h.v.numpy(), new.block_ids)
+        swap.release(h)
+    torch.cuda.synchronize()
+    after = bk._pool.cpu().numpy()
+    for l in range(L):
+        assert np.array_equal(after[l, 0], exp_k[l]) and np.array_equal(after[l, 1], exp_v[l]), l
+    assert swap.num_swapped == 0 and swap.bytes_in_use == 0
+    bk.check_device_errors()

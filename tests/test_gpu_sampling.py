@@ -87,6 +87,19 @@ def test_greedy_strided_and_unaligned_rows():
         assert torch.equal(greedy(view), torch.argmax(view, dim=-1))
 
 
+def test_greedy_overlapping_and_transposed_rows():
+    """Views whose rows overlap in memory (an expanded row: row stride 0; an
+    as_strided view with a row stride below vocab) or whose elements are
+    strided are read through a contiguous copy, never past the allocation."""
+    print("greedy overlapping / transposed rows", flush=True)
+    row = torch.randn(1, 5000, device=DEV).half()
+    flat = torch.randn(6000, device=DEV).half()
+    sq = torch.randn(300, 300, device=DEV)
+    for view in (row.expand(64, 5000), flat.as_strided((8, 5000), (100, 1)), sq.t(),
+                 row.expand(1, 5000)):
+        assert torch.equal(greedy(view), torch.argmax(view, dim=-1))
+
+
 def test_argmax_rows_rejects_bad_arguments():
     lib = _native.load()
     out = torch.empty(2, dtype=torch.int64, device=DEV)

@@ -18,7 +18,6 @@ the benchmark configurations, each against the oracle on the same inputs:
 
 from __future__ import annotations
 
-import dataclasses
 import random
 
 import numpy as np
@@ -29,17 +28,17 @@ from llm_serving_layer_amd import BlockAllocator, SequenceBlocks
 from llm_serving_layer_amd.backend import DEFAULT_PART_PAGES, MI355XBackend
 from oracle import PagedTorchOracle, append_closed_form, copy_blocks_closed_form
 
-from ._util import assert_attention_close, grow_and_assemble, lognormal_lengths
+from ._util import assert_attention_close, grow_and_assemble, lognormal_lengths, meta_to_device
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 SEED = 20260731
 
 
-def _to_dev(meta):
-    return dataclasses.replace(meta, **{f.name: getattr(meta, f.name).to(DEV)
-                                        for f in dataclasses.fields(meta)
-                                        if isinstance(getattr(meta, f.name), torch.Tensor)})
+def _to_dev(meta, mirror=True):
+    """On the device, with the host mirror a serving loop's meta carries
+    (the backend plans from it), unless ``mirror=False``."""
+    return meta_to_device(meta, DEV, mirror)
 
 
 def _shuffled(nb, seed):
@@ -77,8 +76,9 @@ class _Decode:
         meta = grow_and_assemble(self.seqs, [1] * len(self.seqs), 16)
         n = meta.n_tokens
         k, v, q = _half((n, 8, 64), self.g), _half((n, 8, 64), self.g), _half((n, 32, 64), self.g)
-        self.gpu.append_kv(0, k, v, _to_dev(meta))
-        out = self.gpu.attend(q, 0, 0.125, _to_dev(meta))
+        dm = _to_dev(meta)   # one meta for both calls: the append is fused into the attend
+        self.gpu.append_kv(0, k, v, dm)
+        out = self.gpu.attend(q, 0, 0.125, dm)
         self.gpu.check_device_errors()
         self.ref.append_kv(0, k.float().cpu(), v.float().cpu(), meta)
         want = self.ref.attend(q.float().cpu(), 0, 0.125, meta)
@@ -153,8 +153,9 @@ def test_chunked_prefill_8x512_over_shared_1536_prefix():
                == pre.block_ids for i in range(n_seq)), "tables must share the prefix blocks"
     T = meta.n_tokens
     k, v, q = _half((T, 8, 64), g), _half((T, 8, 64), g), _half((T, 32, 64), g)
-    bk.append_kv(0, k, v, _to_dev(meta))
-    out = bk.attend(q, 0, 0.125, _to_dev(meta))
+    dm = _to_dev(meta)
+    bk.append_kv(0, k, v, dm)
+    out = bk.attend(q, 0, 0.125, dm)
     bk.check_device_errors()
     assert bk.q_tile == bk._prefill_tile > 0, "the matrix-core prefill must serve this batch"
     ref.append_kv(0, k.float().cpu(), v.float().cpu(), meta)

@@ -64,3 +64,22 @@ def test_planted_last_of_ties_order_is_caught():
 def test_greedy_rejects_bad_logits_before_launching(bad, match):
     with pytest.raises(ValueError, match=match):
         sampling.greedy(bad)
+
+
+def test_rows_for_kernel_copies_overlapping_or_strided_rows():
+    """The argmax kernel reads row i at i * stride(0) for vocab elements: a
+    view whose rows overlap (expand: row stride 0; as_strided with a row
+    stride below vocab) or whose elements are strided is copied first, and
+    every other layout is passed through without a copy."""
+    base = torch.arange(12.0).reshape(3, 4)
+    assert sampling.rows_for_kernel(base) is base
+    wide = torch.zeros(3, 10)[:, :4]                      # row stride 10 >= vocab
+    assert sampling.rows_for_kernel(wide) is wide
+    one = base[:1].expand(1, 4)
+    assert sampling.rows_for_kernel(one) is one           # a single row never overlaps
+    for view in (base[:1].expand(5, 4),                   # row stride 0
+                 torch.arange(20.0).as_strided((4, 4), (2, 1)),   # row stride 2 < 4
+                 base.t()):                               # element stride 4
+        got = sampling.rows_for_kernel(view)
+        assert got.is_contiguous() and got.stride(0) >= got.shape[1]
+        assert torch.equal(got, view)

@@ -246,3 +246,33 @@ def test_measured_plan_fits_the_free_memory_of_the_device():
     bk = small.backend(device="cuda:0")
     assert bk.num_blocks == small.num_blocks and bk.pool_bytes() == small.bytes_used
     assert bk.block_bytes() == small.bytes_per_block
+    # the plan's decode workspace is allocated up front, for its partition size
+    assert small.workspace_bytes > 0
+    assert bk.workspace_bytes() == small.workspace_bytes
+    assert bk.part_pages == small.part_pages
+
+
+def test_plan_backend_forwards_its_workspace_and_partition_size(monkeypatch):
+    """KVPoolPlan.backend() builds the backend with the decode workspace the
+    plan reserved and the partition size it was reserved for (so a batch
+    within the plan's limits never allocates during a step); explicit
+    keyword arguments still win."""
+    import llm_serving_layer_amd.backend as backend_mod
+
+    seen = {}
+
+    class Recorder:
+        def __init__(self, *args, **kwargs):
+            seen.clear()
+            seen.update(kwargs)
+            seen["args"] = args
+
+    monkeypatch.setattr(backend_mod, "MI355XBackend", Recorder)
+    plan = plan_kv_pool(total_vram_bytes=256 * MIB, model_weight_bytes=0,
+                        activation_headroom_bytes=0, max_batch_seqs=64, part_pages=12)
+    plan.backend(device="cpu")
+    assert seen["decode_workspace_bytes"] == plan.workspace_bytes > 0
+    assert seen["part_pages"] == 12
+    assert seen["args"][:2] == (plan.shape.n_layers, plan.num_blocks)
+    plan.backend(device="cpu", part_pages=20, decode_workspace_bytes=0)
+    assert seen["part_pages"] == 20 and seen["decode_workspace_bytes"] == 0

@@ -9,6 +9,7 @@ shared device array is reused with the first call's contents still in it.
 from __future__ import annotations
 
 import ctypes as C
+import gc
 
 import pytest
 import torch
@@ -104,3 +105,54 @@ def test_noalloc_rejects_a_plan_beyond_its_array():
     assert b"at most" in lib.pkv_last_error()
     torch.cuda.synchronize()
     assert int(dummy.abs().sum()) == 0, "nothing may have run"
+
+
+def test_noalloc_allocates_nothing_and_replays_from_a_graph():
+    """What the entry point is for: after a first call on the device (which
+    looks up the array's address), a call changes neither torch's allocated
+    bytes nor the device's free memory, and the call captured into a HIP
+    graph replays (three times, with eager work between) to the bits of an
+    eager call."""
+    print("noalloc: no allocation, graph capture and replay", flush=True)
+    lib = _native.load()
+    lens = lognormal_lengths(256, 256, 0.8, 2048, 20260731)
+    nb = 2 * sum(-(-n // 16) for n in lens) + 16
+    (_, bk), (_, p), q, k, v = _batch(lens, nb, 21, True)
+    assert p.n_slots > 0
+    eager = torch.empty_like(q)
+    _native.check(_call(lib, "pkv_attend_decode_noalloc", bk, p, q, eager, k, v, False),
+                  "pkv_attend_decode_noalloc")          # warm-up: the address lookup
+    torch.cuda.synchronize()
+    again = torch.full_like(q, float("nan"))
+    # Torch's allocator counts every allocation it makes (cumulatively), and
+    # an allocation outside it (hipMalloc) would take device memory: neither
+    # may move. (Frees of earlier tensors whose release the allocator
+    # deferred may still land inside the window and only raise free memory.)
+    gc.collect()
+    gc.disable()
+    try:
+        torch.cuda.synchronize()
+        made0 = torch.cuda.memory_stats(DEV)["allocation.all.allocated"]
+        free0, _ = torch.cuda.mem_get_info(DEV)
+        _native.check(_call(lib, "pkv_attend_decode_noalloc", bk, p, q, again, k, v, False),
+                      "pkv_attend_decode_noalloc")
+        torch.cuda.synchronize()
+        free1, _ = torch.cuda.mem_get_info(DEV)
+        made1 = torch.cuda.memory_stats(DEV)["allocation.all.allocated"]
+    finally:
+        gc.enable()
+    assert made1 == made0, f"torch made {made1 - made0} allocations during the call"
+    assert free1 >= free0, f"device free memory fell by {free0 - free1} bytes"
+    assert torch.equal(again, eager)
+    replayed = torch.full_like(q, float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _native.check(_call(lib, "pkv_attend_decode_noalloc", bk, p, q, replayed, k, v, False),
+                      "pkv_attend_decode_noalloc (captured)")
+    for rep in range(3):
+        replayed.fill_(float("nan"))
+        torch.randn(1 << 20, device=DEV).sum().item()   # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        bk.check_device_errors()
+        assert torch.equal(replayed, eager), f"replay {rep} differs from the eager call"
