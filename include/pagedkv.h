@@ -75,8 +75,11 @@ int pkv_append_kv(void* k_pool, void* v_pool, int64_t num_slots,
  * (PKV_ERR_INVALID, message naming kv_last_page_len, as
  * serving/backends/paged_torch.py:379-392 does).
  *
- * Each sequence of np pages is cut into ceil(np / part_pages) pieces of
- * nearly equal size (a function of its own length only); the pieces are
+ * Each sequence of np pages is cut into pieces of part_pages pages, the
+ * remainder last, a remainder shorter than both 4 pages and half a piece
+ * joining the piece before it (a function of its own length only: at most
+ * ceil(np / part_pages) pieces of at most part_pages + 3 pages); the pieces
+ * are
  * dealt longest first to the least-loaded of at most
  * max_workgroups / (n_kv_heads / heads-per-workgroup) bins. The plan is
  * bins blocks of *plan_stride_out ints: {n_items, n_pages, 0, 0}, n_pages

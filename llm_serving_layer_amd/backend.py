@@ -46,7 +46,7 @@ import torch
 
 from . import _native
 from .contract import BatchMeta
-from .sizing import DEFAULT_PART_PAGES  # split-K partition: 20 pages = 320 tokens
+from .sizing import DEFAULT_PART_PAGES  # split-K pieces: 17 pages = 272 tokens
 
 __all__ = ["MI355XBackend", "is_available", "unavailable_reason"]
 

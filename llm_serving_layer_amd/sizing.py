@@ -51,9 +51,9 @@ DEFAULT_BLOCK_SIZE = 16
 #: Largest batch the decode workspace is reserved for by default: the
 #: 4096-sequence capacity workload.
 DEFAULT_MAX_BATCH_SEQS = 4096
-# Split-K partition of the decode kernel, in pages (320 tokens): the
+# Split-K piece size of the decode kernel, in pages (272 tokens): the
 # backend's default, so the workspace reserved here is the one it uses.
-DEFAULT_PART_PAGES = 20
+DEFAULT_PART_PAGES = 17
 #: Longest sequence the decode workspace is reserved for by default (the
 #: reference's max_seq, bench/capacity.py:196-242).
 DEFAULT_MAX_SEQ_LEN = 2048

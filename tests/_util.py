@@ -189,3 +189,18 @@ def meta_to_device(meta: BatchMeta, device, mirror: bool = True) -> BatchMeta:
     out = dataclasses.replace(meta, **moved, host=host)
     assert (out.host_arrays() is not None) == mirror
     return out
+
+
+def expected_cut(n_pages: int, part_pages: int) -> list:
+    """Piece sizes of a sequence of ``n_pages`` pages as the decode planner
+    cuts it: pieces of ``part_pages`` pages, the remainder last, a remainder
+    shorter than both 4 pages and half a piece joining the piece before it."""
+    full, rem = divmod(n_pages, part_pages)
+    if full == 0:
+        return [rem]
+    sizes = [part_pages] * full
+    if 0 < rem < min(4, (part_pages + 1) // 2):
+        sizes[-1] += rem
+    elif rem:
+        sizes.append(rem)
+    return sizes

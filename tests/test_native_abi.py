@@ -19,7 +19,7 @@ import torch
 from llm_serving_layer_amd import _native
 from llm_serving_layer_amd.backend import MI355XBackend
 
-from ._util import plan_decode
+from ._util import expected_cut, plan_decode
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "pagedkv.h"
 
@@ -52,8 +52,9 @@ def _role(it):
 @pytest.mark.parametrize("workgroups", [1, 96, 512])
 def test_decode_plan_covers_every_page_once(part_pages, workgroups):
     """Every page of every sequence is in exactly one piece of one bin, with
-    its id and live row count; pieces of a sequence are consecutive and
-    nearly equal (sizes differ by at most one page); in a bin, pieces of cut
+    its id and live row count; pieces of a sequence are consecutive, of
+    part_pages pages with the remainder last (a remainder below 4 pages
+    joins the piece before it); in a bin, pieces of cut
     sequences before their last come first and last pieces last; the partial
     slots of cut sequences are dense and unique, so no two pieces share one,
     and every (sequence, head) arrival counter index stays below
@@ -75,8 +76,8 @@ def test_decode_plan_covers_every_page_once(part_pages, workgroups):
         for it in items:
             seq, first = it["seq"], it["tok0"] // 16
             assert 0 <= seq < len(kv_lens) and it["kv"] == kv_lens[seq] and it["tok0"] % 16 == 0
-            k = -(-npages[seq] // part_pages)
-            assert it["nparts"] == k and 1 <= it["np"] <= part_pages
+            k = len(expected_cut(int(npages[seq]), part_pages))
+            assert it["nparts"] == k and 1 <= it["np"] <= part_pages + 3
             assert it["last"] == (first + it["np"] == npages[seq])
             for t, (pid, live, bad) in enumerate(it["pages"]):
                 pg = first + t
@@ -93,7 +94,7 @@ def test_decode_plan_covers_every_page_once(part_pages, workgroups):
     for seq, ps_ in by_seq.items():
         ps_.sort()
         sz = [n for _, n, _, _ in ps_]
-        assert max(sz) - min(sz) <= 1, "pieces of a sequence are nearly equal"
+        assert sz == expected_cut(int(npages[seq]), part_pages), "the planner's cut"
         if len(ps_) > 1:  # slot = first slot + piece index, in page order
             assert [s - s0 for _, _, s, s0 in ps_] == list(range(len(ps_)))
 
@@ -310,3 +311,20 @@ def test_decode_plan_falls_back_to_larger_pieces_past_2gib_of_partials():
     need = bk._lib.pkv_decode_workspace_bytes(n, n_slots, 32, 8, 64)
     assert need < 2**31
     assert bk._lib.pkv_decode_workspace_bytes(n, n * pages // 2, 32, 8, 64) > 2**31
+
+
+@pytest.mark.parametrize("n_pages, sizes", [
+    (5, [5]), (17, [17]), (18, [18]), (20, [20]), (21, [17, 4]), (34, [17, 17]),
+    (36, [17, 19]), (40, [17, 17, 6]), (86, [17, 17, 17, 17, 18])])
+def test_decode_plan_cut_known_answers(n_pages, sizes):
+    """The planner's pieces of one sequence at 17-page partitions, in page
+    order: full pieces first, the remainder last, a remainder of 1..3
+    pages joined to the piece before it (and at 2-page partitions, where
+    half a piece is one page, no remainder is joined)."""
+    _, bins, _, n_slots = plan_decode([16 * n_pages], 17, 512)
+    got = sorted((it["tok0"] // 16, it["np"]) for b in bins for it in b)
+    assert [n for _, n in got] == sizes == expected_cut(n_pages, 17)
+    assert n_slots == (len(sizes) if len(sizes) > 1 else 0)
+    _, bins, _, _ = plan_decode([16 * n_pages], 2, 512)
+    got = sorted((it["tok0"] // 16, it["np"]) for b in bins for it in b)
+    assert [n for _, n in got] == [2] * (n_pages // 2) + [1] * (n_pages % 2)
