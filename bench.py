@@ -266,29 +266,65 @@ def check_layers_vs_oracle(ctx, layers=(0, LAYERS - 1)):
 
 def time_e2e(ctx, step, steps, warmup):
     """
-    Serving-loop step: build this step's BatchMeta from the scheduler's
-    sequence state, plan it, and enqueue the 16 layers, with no host wait
-    inside the loop, so building step n+1 overlaps the GPU running step n.
-    The same sequences are re-described every step (the work per step stays
-    the headline's). Wall time per step after a final synchronization.
+    Serving-loop step, as the reference's scheduler runs one
+    (serving/scheduler/scheduler.py:743-757): grow every sequence by the
+    token it is about to write and describe the batch (DecodeStepper: one
+    allocate call for the sequences whose last page is full, the CSR and
+    the other index arrays updated in place, one pinned upload), plan the
+    step, and enqueue its 16 layers (append_kv + attend each), with no host
+    wait inside the loop, so step n+1's host work overlaps the GPU running
+    step n.
+
+    Each step holds one more token per sequence than the one before, so the
+    loop is compared with the GPU time of the same work: the step issued
+    eagerly with fixed metadata (no host work but the enqueue), timed at
+    the lengths the loop starts from and at those it ends at (the work is
+    linear in the tokens; their mean is the loop's mean GPU step).
+    Returns (wall ms per loop step, that GPU ms per step, host ms of each
+    part of a loop step, measured in separate loops).
     """
     import torch
     from llm_serving_layer_amd import ScheduledSeq, build_batch_meta
+    from llm_serving_layer_amd.stepping import DecodeStepper
 
-    seqs = ctx["seqs"]
+    bk, seqs = ctx["bk"], ctx["seqs"]
+    stepper = DecodeStepper(seqs, "cuda:0", BS)
 
     def one():
+        step(None, stepper.step())
+
+    def gpu_step_here():
         m = build_batch_meta([ScheduledSeq(s, [0]) for s in seqs], "cuda:0", BS)
-        step(None, m)
+        return time_eager(lambda ev: step(ev, m), steps, warmup, LAYERS)["gpu_ms_per_step"]
 
     for _ in range(warmup):
         one()
     torch.cuda.synchronize()
+    gpu_start = gpu_step_here()
     t0 = time.perf_counter()
     for _ in range(steps):
         one()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps
+    e2e_ms = (time.perf_counter() - t0) * 1e3 / steps
+    gpu_end = gpu_step_here()
+    # the parts, each over `steps` repetitions (host time only)
+    parts = {}
+    t0 = time.perf_counter()
+    metas = [stepper.step() for _ in range(steps)]
+    parts["grow_and_describe"] = (time.perf_counter() - t0) * 1e3 / steps
+    t0 = time.perf_counter()
+    for m in metas:
+        bk._ensure_planned(m)
+    parts["plan"] = (time.perf_counter() - t0) * 1e3 / steps
+    torch.cuda.synchronize()
+    m = metas[-1]
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(None, m)
+    parts["enqueue_16_layers"] = (time.perf_counter() - t0) * 1e3 / steps
+    torch.cuda.synchronize()
+    return (e2e_ms, (gpu_start + gpu_end) / 2,
+            {k: round(v, 4) for k, v in parts.items()})
 
 
 def run_decode_like(args, lens, nb, label, check=False, e2e=False):
@@ -330,7 +366,8 @@ def run_decode_like(args, lens, nb, label, check=False, e2e=False):
             parity["graph_replay_max_abs_vs_oracle"] = graph_parity["max_abs_vs_oracle"]
     else:
         parity = None
-    e2e_ms = time_e2e(ctx, step, args.steps, args.warmup) if e2e else None
+    e2e_ms, e2e_gpu, e2e_parts = (time_e2e(ctx, step, args.steps, args.warmup) if e2e
+                                  else (None, None, None))
     ms = eager["ms_per_step"]
     # per launch: the GPU time of a step over its 16 launches (gaps between
     # launches included)
@@ -341,7 +378,8 @@ def run_decode_like(args, lens, nb, label, check=False, e2e=False):
         "gbps": gbps, "ms": ms, "tok_s": len(lens) / (ms * 1e-3), "pages": pages,
         "step_bytes": step_bytes, "layer_bytes": layer_bytes, "launch_ms": launch_ms,
         "kern_gbps": kern_gbps, "eager": eager, "graph": graph, "meta_ms": meta_ms,
-        "plan_ms": plan_ms, "parity": parity, "e2e_ms": e2e_ms,
+        "plan_ms": plan_ms, "parity": parity, "e2e_ms": e2e_ms, "e2e_parts": e2e_parts,
+        "e2e_gpu_ms": e2e_gpu,
     }
 
 
@@ -375,10 +413,12 @@ def bench_decode(args):
                          "plan": round(r["plan_ms"], 3)},
         "e2e": {"ms_per_step": round(r["e2e_ms"], 4),
                 "decode_tok_s": round(256 / (r["e2e_ms"] * 1e-3), 1),
-                "ratio_to_gpu_step": round(r["e2e_ms"] / r["ms"], 3),
-                "what": ("per step: build_batch_meta from the sequences' block tables, plan, "
-                         "16 x (append_kv + attend) enqueued call by call; no host wait "
-                         "inside the loop")},
+                "gpu_ms_per_step_same_lengths": round(r["e2e_gpu_ms"], 4),
+                "ratio_to_gpu_step": round(r["e2e_ms"] / r["e2e_gpu_ms"], 3),
+                "host_ms_per_step": r["e2e_parts"],
+                "what": ("per step: every sequence grown by one token and the batch described "
+                         "(DecodeStepper), planned, 16 x (append_kv + attend) enqueued call by "
+                         "call; no host wait inside the loop")},
         "parity": r["parity"],
         "roofline": {
             "kernel": "pkv::decode_kernel<_Float16,64,4> (LPT bins of (sequence, piece) items, split-K merge by the last arriver, KV append fused), one launch per layer",
@@ -596,7 +636,7 @@ def bench_capacity(args):
     phase_b = lognormal_lengths(512, 2048)
     out = {}
     for name, lens in (("A", phase_a), ("B", phase_b)):
-        r = run_decode_like(args, lens, nb, f"capacity phase {name}")
+        r = run_decode_like(args, lens, nb, f"capacity phase {name}", e2e=name == "A")
         out[name] = {"sequences": len(lens), "mean_len": round(sum(lens) / len(lens), 1),
                      "tokens": sum(lens), "pages": r["pages"], "ms_per_step": round(r["ms"], 4),
                      "GB/s": round(r["gbps"], 1),
@@ -605,6 +645,11 @@ def bench_capacity(args):
                      "launch_ms": round(r["launch_ms"], 5),
                      "graph_replay_ms_per_step": (round(r["graph"]["ms_per_step"], 4)
                                                   if r["graph"] else None)}
+        if r["e2e_ms"] is not None:
+            out[name]["e2e"] = {"ms_per_step": round(r["e2e_ms"], 4),
+                                "gpu_ms_per_step_same_lengths": round(r["e2e_gpu_ms"], 4),
+                                "ratio_to_gpu_step": round(r["e2e_ms"] / r["e2e_gpu_ms"], 3),
+                                "host_ms_per_step": r["e2e_parts"]}
         del r
         torch.cuda.empty_cache()
     total_bytes = sum(LAYERS * decode_bytes(l, sum(-(-n // BS) for n in l))

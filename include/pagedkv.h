@@ -252,6 +252,19 @@ int pkv_copy_blocks(void* pool_base, int32_t n_layers, int64_t plane_bytes,
                     int32_t* status_word, void* stream);
 
 /*
+ * Metadata upload — replaces the host-to-device tensor builds of
+ * build_batch_meta (serving/engine_iface/batch.py:246-318; one pinned buffer
+ * per step here): `bytes` bytes of the pinned host buffer `host` (allocated
+ * pinned, hence mapped for the device) are copied to device memory `dst` by
+ * a kernel on `stream` that reads the buffer through its device mapping, so
+ * the copy is ordered on the launch stream like the kernels that read it,
+ * with no copy-engine hand-off. `host` must stay unchanged until the copy
+ * has run (the caller records an event after it). PKV_ERR_INVALID if `host`
+ * is not pinned memory mapped for the device.
+ */
+int pkv_upload_pinned(void* dst, const void* host, int64_t bytes, void* stream);
+
+/*
  * Swap-out gather — the device half of KVSwapSpace._to_host
  * (serving/scheduler/preemption.py:490-509): staging[kv][layer][i] = block
  * ids[i] of plane (layer, kv), i.e. staging is [2][n_layers][n_ids][block]

@@ -15,7 +15,7 @@ from pathlib import Path
 # PKV_LIBRARY selects another build of the same library (e.g. a tuning variant).
 LIB_PATH = Path(os.environ.get("PKV_LIBRARY") or
                 Path(__file__).resolve().parent / "_native" / "libpagedkv.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 DECODE_SCRATCH_BYTES = 64 * 1024 * 1024   # PKV_DECODE_SCRATCH_BYTES
@@ -49,6 +49,7 @@ SIGNATURES = {
     "pkv_gather_blocks": (C.c_int, [_p, _i32, _i64, _i64, _i64, _p, _i32, _p, _p, _p]),
     "pkv_scatter_blocks": (C.c_int, [_p, _i32, _i64, _i64, _i64, _p, _i32, _p, _p, _p]),
     "pkv_argmax_rows": (C.c_int, [_p, _i64, _i64, _i64, _i32, _p, _p]),
+    "pkv_upload_pinned": (C.c_int, [_p, _p, _i64, _p]),
 }
 
 _LIB = None

@@ -9,8 +9,8 @@ are absolute (``kv_len - q .. kv_len - 1``), the CSR triple comes from
 ``page_size``).
 
 Different from the reference in two respects that matter on MI355X: all ten
-index arrays are packed into ONE pinned host buffer and uploaded with ONE
-non-blocking copy, then exposed as views (ten separate ``torch.tensor(...,
+index arrays (the int64 positions included) are packed into ONE pinned host
+buffer and uploaded with ONE non-blocking copy, then exposed as views (ten separate ``torch.tensor(...,
 device=...)`` calls are ten synchronous H2D round trips per step); and the
 host arrays stay attached to the meta (``BatchMeta.host``), so a backend
 plans the step from them instead of copying the device tensors back.
@@ -27,6 +27,7 @@ import torch
 
 from .contract import MIRRORED, BatchMeta, HostMirror, validate_host
 from .paging import SequenceBlocks
+from .upload import uploader
 
 _BLOCKS = attrgetter("blocks")
 _NEW_IDS = attrgetter("new_token_ids")
@@ -147,28 +148,31 @@ def build_batch_meta(seqs: list[ScheduledSeq], device, page_size: int,
 
 
 def _upload(parts: dict, positions: np.ndarray, device, dtype_index: torch.dtype) -> dict:
-    """Pack every index array into one host buffer, move it once, slice views."""
+    """Pack every index array and the int64 positions into one pinned host
+    buffer, move it with one upload (upload.py), and expose typed views of
+    the device copy."""
     device = torch.device(device)
     idx_np = {torch.int32: np.int32, torch.int64: np.int64}[dtype_index]
+    isz = np.dtype(idx_np).itemsize
     names = list(parts)
     sizes = [parts[k].shape[0] for k in names]
     total = sum(sizes)
-    host = torch.empty(total, dtype=dtype_index,
-                       pin_memory=device.type == "cuda" and torch.cuda.is_available())
-    hv = host.numpy()
+    pos_off = -(-total * isz // 8) * 8            # positions start 8-byte aligned
+    nbytes = pos_off + 8 * positions.shape[0]
+    up = uploader(device) if device.type == "cuda" else None
+    host = up.buffer(nbytes) if up is not None else torch.empty(nbytes, dtype=torch.uint8)
+    hb = host.numpy()
+    hv = hb[:total * isz].view(idx_np)
     off = 0
     for k, sz in zip(names, sizes):
-        hv[off:off + sz] = parts[k].astype(idx_np, copy=False)
+        hv[off:off + sz] = parts[k]
         off += sz
-    pos_host = torch.from_numpy(positions.astype(np.int64, copy=False))
-    if device.type == "cuda":
-        dev = host.to(device, non_blocking=True)
-        pos_dev = pos_host.to(device, non_blocking=True)
-    else:
-        dev, pos_dev = host, pos_host
+    hb[pos_off:].view(np.int64)[:] = positions
+    dev = up.send(host) if up is not None else host
+    idx = dev[:total * isz].view(dtype_index)
     out, off = {}, 0
     for k, sz in zip(names, sizes):
-        out[k] = dev[off:off + sz]
+        out[k] = idx[off:off + sz]
         off += sz
-    out["positions"] = pos_dev
+    out["positions"] = dev[pos_off:].view(torch.int64)
     return out

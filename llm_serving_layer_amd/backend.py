@@ -46,6 +46,7 @@ import torch
 
 from . import _native
 from .contract import BatchMeta
+from .upload import uploader
 from .sizing import DEFAULT_PART_PAGES  # split-K pieces: 17 pages = 272 tokens
 
 __all__ = ["MI355XBackend", "is_available", "unavailable_reason"]
@@ -269,6 +270,9 @@ class MI355XBackend:
         self._workspace = ws
         self._ws_ptr = ws.data_ptr() if ws.numel() else None
         self._ws_bytes = ws.numel()
+        # leading bytes known to be zero between launches (a new workspace
+        # is zero-filled)
+        self._ws_zero = ws.numel()
 
     def check_device_errors(self) -> None:
         """
@@ -610,11 +614,17 @@ class MI355XBackend:
                 break
             part_pages = min(2 * part_pages, MAX_PART_PAGES)
         if need > self._workspace.numel():
-            # zero-filled: the arrival counters at the front start at zero
-            self._set_workspace(torch.zeros(need, dtype=torch.uint8, device=self.device))
-        elif need > 0:
-            # a previous layout may have left partial data where counters now sit
-            self._workspace[:counter_bytes].zero_()
+            # zero-filled (the arrival counters at the front start at zero),
+            # with room to spare: a running batch's plans grow step by step
+            # as its sequences do, and each regrowth is an allocation
+            grown = max(need, self._workspace.numel() * 5 // 4)
+            self._set_workspace(torch.zeros(grown, dtype=torch.uint8, device=self.device))
+        elif counter_bytes > self._ws_zero:
+            # the counters now reach over bytes an earlier layout used for
+            # partials: clear what is new (every counter is zero after a launch)
+            self._workspace[self._ws_zero:counter_bytes].zero_()
+        # after this plan's launch the bytes past its counters hold partials
+        self._ws_zero = counter_bytes
         return (buf[:int(needed.value)].copy(), n_work.value, n_slots.value, stride.value)
 
     def _decode_rows(self, dec, cu, indptr, kvl, last, indices, indices_dev) -> _DecodeRows:
@@ -637,9 +647,9 @@ class MI355XBackend:
         return d
 
     def _upload(self, a: np.ndarray) -> torch.Tensor:
-        """Host array to the device through pinned memory, queued on the
-        current stream without a host wait."""
-        return torch.from_numpy(a).pin_memory().to(self.device, non_blocking=True)
+        """Host array to the device through a pinned ring buffer, uploaded by a
+        kernel on the current stream without a host wait (upload.py)."""
+        return uploader(self.device).array(a)
 
     def invalidate_plan(self) -> None:
         """Force the next ``attend`` to re-plan (and drop the cached meta)."""

@@ -6,6 +6,8 @@
 #include <cstdarg>
 #include <cstring>
 
+#include <algorithm>
+
 #include "pkv_common.h"
 
 namespace pkv {
@@ -151,13 +153,50 @@ static int launch_blocks(char* pool, int32_t n_layers, int64_t plane_bytes,
   return PKV_OK;
 }
 
+// One step's metadata from a pinned host buffer to the device, read by the
+// kernel through the buffer's device mapping: the copy is an ordinary
+// kernel on the caller's stream, so the next kernel does not wait for a
+// hand-off from a copy engine. 16-byte chunks when both ends and the size
+// allow it, bytes otherwise.
+template <typename V>
+__global__ __launch_bounds__(256) void upload_kernel(V* __restrict__ dst,
+                                                     const V* __restrict__ src, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
 }  // namespace pkv
 
 using namespace pkv;
 
 extern "C" {
 
-int pkv_abi_version(void) { return 10; }
+int pkv_upload_pinned(void* dst, const void* host, int64_t bytes, void* stream) {
+  if (bytes < 0) return fail(PKV_ERR_INVALID, "negative byte count");
+  if (bytes == 0) return PKV_OK;
+  if (!dst || !host) return fail(PKV_ERR_INVALID, "null buffer");
+  void* src = nullptr;
+  // only pinned memory the runtime maps for the device has a device pointer
+  const hipError_t e = hipHostGetDevicePointer(&src, const_cast<void*>(host), 0);
+  if (e != hipSuccess || !src)
+    return fail(PKV_ERR_INVALID, "the source is not pinned host memory mapped for the device "
+                "(%s)", hipGetErrorString(e));
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = ((uintptr_t)dst | (uintptr_t)src | (uintptr_t)bytes) % 16 == 0;
+  const int64_t n = vec ? bytes / 16 : bytes;
+  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 1024);
+  if (vec)
+    hipLaunchKernelGGL((upload_kernel<v4i>), dim3(grid), dim3(256), 0, s, (v4i*)dst,
+                       (const v4i*)src, n);
+  else
+    hipLaunchKernelGGL((upload_kernel<unsigned char>), dim3(grid), dim3(256), 0, s,
+                       (unsigned char*)dst, (const unsigned char*)src, n);
+  PKV_LAUNCH_CHECK();
+  return PKV_OK;
+}
+
+int pkv_abi_version(void) { return 11; }
 
 const char* pkv_last_error(void) { return g_err.c_str(); }
 

@@ -301,6 +301,7 @@ def test_decode_plan_falls_back_to_larger_pieces_past_2gib_of_partials():
 
     bk = _host_backend(part_pages=1)
     bk._workspace = _Reserved()
+    bk._ws_zero = 0
     n, pages = 4096, 128
     indptr = np.arange(0, (n + 1) * pages, pages, dtype=np.int32)
     indices = np.arange(n * pages, dtype=np.int32) % 64
