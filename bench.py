@@ -214,14 +214,17 @@ def decode_setup(device, lens, nb, part_pages):
     v = (torch.randn(LAYERS, T, HKV, D, generator=g, device=device) * 0.5).half()
     q = (torch.randn(LAYERS, T, HQ, D, generator=g, device=device) * 0.5).half()
     outs = [None] * LAYERS   # the last step's attention outputs, per layer
+    # each layer's q, k, v as a tensor of its own (as a model's projections
+    # hand them over), not sliced inside the timed loop
+    qs, ks, vs = list(q.unbind(0)), list(k.unbind(0)), list(v.unbind(0))
 
     def step(events, m=None):
         m = meta if m is None else m
         for l in range(LAYERS):
-            bk.append_kv(l, k[l], v[l], m)
+            bk.append_kv(l, ks[l], vs[l], m)
             if events is not None:
                 events[l][0].record()
-            outs[l] = bk.attend(q[l], l, 0.125, m)
+            outs[l] = bk.attend(qs[l], l, 0.125, m)
             if events is not None:
                 events[l][1].record()
 
@@ -273,15 +276,18 @@ def time_e2e(ctx, step, steps, warmup):
     the other index arrays updated in place, one pinned upload), plan the
     step, and enqueue its 16 layers (append_kv + attend each), with no host
     wait inside the loop, so step n+1's host work overlaps the GPU running
-    step n.
+    step n. After `warmup` free-running steps, `steps` steps are timed with
+    HIP events on the launch stream (the host's own time for them is
+    reported beside it: below the GPU's, the loop is GPU-bound).
 
     Each step holds one more token per sequence than the one before, so the
     loop is compared with the GPU time of the same work: the step issued
     eagerly with fixed metadata (no host work but the enqueue), timed at
-    the lengths the loop starts from and at those it ends at (the work is
-    linear in the tokens; their mean is the loop's mean GPU step).
-    Returns (wall ms per loop step, that GPU ms per step, host ms of each
-    part of a loop step, measured in separate loops).
+    the lengths the loop starts from and at those it ends at, and
+    interpolated (the work is linear in the tokens) to the timed steps'
+    mean length.
+    Returns (ms per loop step, that GPU ms per step, host ms of each part of
+    a loop step, measured in separate loops).
     """
     import torch
     from llm_serving_layer_amd import ScheduledSeq, build_batch_meta
@@ -297,15 +303,21 @@ def time_e2e(ctx, step, steps, warmup):
         m = build_batch_meta([ScheduledSeq(s, [0]) for s in seqs], "cuda:0", BS)
         return time_eager(lambda ev: step(ev, m), steps, warmup, LAYERS)["gpu_ms_per_step"]
 
+    gpu_start = gpu_step_here()
+    # steady state: the loop runs free (no host wait); the timed steps are
+    # bracketed by HIP events on the launch stream, so the figure is the GPU
+    # timeline of those steps, including any time the GPU waits for the host
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for _ in range(warmup):
         one()
-    torch.cuda.synchronize()
-    gpu_start = gpu_step_here()
+    start.record()
     t0 = time.perf_counter()
     for _ in range(steps):
         one()
+    stop.record()
+    host_ms = (time.perf_counter() - t0) * 1e3 / steps
     torch.cuda.synchronize()
-    e2e_ms = (time.perf_counter() - t0) * 1e3 / steps
+    e2e_ms = start.elapsed_time(stop) / steps
     gpu_end = gpu_step_here()
     # the parts, each over `steps` repetitions (host time only)
     parts = {}
@@ -323,7 +335,11 @@ def time_e2e(ctx, step, steps, warmup):
         step(None, m)
     parts["enqueue_16_layers"] = (time.perf_counter() - t0) * 1e3 / steps
     torch.cuda.synchronize()
-    return (e2e_ms, (gpu_start + gpu_end) / 2,
+    parts["loop_host_ms_per_step"] = host_ms
+    # the GPU step at the timed steps' mean length (warmup + steps / 2 tokens
+    # past the start; gpu_end is warmup + steps past it)
+    gpu_ref = gpu_start + (gpu_end - gpu_start) * (warmup + steps / 2) / (warmup + steps)
+    return (e2e_ms, gpu_ref,
             {k: round(v, 4) for k, v in parts.items()})
 
 
