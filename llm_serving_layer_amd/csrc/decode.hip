@@ -481,19 +481,27 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   };
 
   // lane (dim column n, group g) holds heads 4g..4g+3 of dims 16b + n.
-  auto write_out = [&](int sq) __attribute__((always_inline)) {
+  auto write_out = [&](int sq, const f32x4* oo, float ll) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * g + i;
-      const float li = from_lane(l_run, i);  // lane r holds head r's sum
+      const float li = from_lane(ll, i);  // lane r holds head r's sum
       if (r < G) {
         const float inv = 1.f / li;   // one division per row, not per element
 #pragma unroll
         for (int b = 0; b < NDB; ++b)
-          out[((int64_t)sq * Hq + h * G + r) * D + 16 * b + n] = (T)(o[b][i] * inv);
+          out[((int64_t)sq * Hq + h * G + r) * D + 16 * b + n] = (T)(oo[b][i] * inv);
       }
     }
   };
+  // A whole sequence's output, held until the next step has copied its page
+  // and writes it before sending that step's page loads: stores issued after
+  // a page's loads would make the single wait at the top of the loop, which
+  // serves every path, also wait for them (a store round trip per item);
+  // issued before them, they complete within the wait for the page.
+  f32x4 wo_o[NDB];
+  float wo_l = 1.f;
+  int wo_seq = -1;   // -1: nothing held
 
   // The current item's last page: write the new row (fused append) and patch
   // the loaded copy when slot_mapping agrees with the page table.
@@ -560,7 +568,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   // Item end: the output (whole sequence), or the partial of a cut sequence.
   auto end_item = [&](int p) __attribute__((always_inline)) {
     if (cur.slot < 0) {
-      write_out(cur.seq);
+      wo_seq = cur.seq;
+      wo_l = l_run;
+#pragma unroll
+      for (int b = 0; b < NDB; ++b) wo_o[b] = o[b];
     } else {
       flush_arrival();   // at most one deferred arrival at a time
       const bool last = cur.flags & kItemLast;
@@ -689,6 +700,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wcur = wnext;
     wnext = words[p + 2];   // inside the plan block: its words are followed by items
+    if (wo_seq >= 0) {      // the previous item's output, before this step's loads
+      write_out(wo_seq, wo_o, wo_l);
+      wo_seq = -1;
+    }
     load_page(p + 1, wcur, kr, vr);
     compute(p);
     PKV_TL(if (p == 0) tl_first = __builtin_amdgcn_s_memrealtime();)
@@ -705,6 +720,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     wave_lds_sync();  // this page's tile reads are done before the next copy
   }
   PKV_TL(const unsigned long long tl_last = __builtin_amdgcn_s_memrealtime();)
+  if (wo_seq >= 0) write_out(wo_seq, wo_o, wo_l);
   flush_arrival();
 #ifdef PKV_TIMELINE
   {
