@@ -402,7 +402,7 @@ def run_decode_like(args, lens, nb, label, check=False, e2e=False):
 def bench_decode(args):
     lens = lognormal_lengths(256, 256)
     r = run_decode_like(args, lens, 2 * sum(-(-n // BS) for n in lens), "decode",
-                        check=True, e2e=True)
+                        check=True, e2e=not args.no_e2e)
     e = r["eager"]
     line = base_line(
         args, METRIC, round(r["gbps"], 1), "GB/s", r["ms"], "fp16",
@@ -427,14 +427,15 @@ def bench_decode(args):
             "what": "the same step captured once in a HIP graph and replayed"},
         "host_side_ms": {"batch_meta_build_upload": round(r["meta_ms"], 3),
                          "plan": round(r["plan_ms"], 3)},
-        "e2e": {"ms_per_step": round(r["e2e_ms"], 4),
-                "decode_tok_s": round(256 / (r["e2e_ms"] * 1e-3), 1),
-                "gpu_ms_per_step_same_lengths": round(r["e2e_gpu_ms"], 4),
-                "ratio_to_gpu_step": round(r["e2e_ms"] / r["e2e_gpu_ms"], 3),
-                "host_ms_per_step": r["e2e_parts"],
-                "what": ("per step: every sequence grown by one token and the batch described "
-                         "(DecodeStepper), planned, 16 x (append_kv + attend) enqueued call by "
-                         "call; no host wait inside the loop")},
+        "e2e": None if r["e2e_ms"] is None else {
+            "ms_per_step": round(r["e2e_ms"], 4),
+            "decode_tok_s": round(256 / (r["e2e_ms"] * 1e-3), 1),
+            "gpu_ms_per_step_same_lengths": round(r["e2e_gpu_ms"], 4),
+            "ratio_to_gpu_step": round(r["e2e_ms"] / r["e2e_gpu_ms"], 3),
+            "host_ms_per_step": r["e2e_parts"],
+            "what": ("per step: every sequence grown by one token and the batch described "
+                     "(DecodeStepper), planned, 16 x (append_kv + attend) enqueued call by "
+                     "call; no host wait inside the loop")},
         "parity": r["parity"],
         "roofline": {
             "kernel": "pkv::decode_kernel<_Float16,64,4> (LPT bins of (sequence, piece) items, split-K merge by the last arriver, KV append fused), one launch per layer",
@@ -652,7 +653,8 @@ def bench_capacity(args):
     phase_b = lognormal_lengths(512, 2048)
     out = {}
     for name, lens in (("A", phase_a), ("B", phase_b)):
-        r = run_decode_like(args, lens, nb, f"capacity phase {name}", e2e=name == "A")
+        r = run_decode_like(args, lens, nb, f"capacity phase {name}",
+                            e2e=name == "A" and not args.no_e2e)
         out[name] = {"sequences": len(lens), "mean_len": round(sum(lens) / len(lens), 1),
                      "tokens": sum(lens), "pages": r["pages"], "ms_per_step": round(r["ms"], 4),
                      "GB/s": round(r["gbps"], 1),
@@ -964,6 +966,9 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true",
                     help="decode: report the call-by-call step, no graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the serving loop (its steps grow the sequences; profiles of "
+                         "the headline step leave it out)")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU work per CPU-baseline thread setting")
     args = ap.parse_args()
