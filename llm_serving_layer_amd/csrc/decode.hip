@@ -345,6 +345,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     return Item{it[0], it[1], it[2], it[3], it[4], it[5], it[6], it[7]};
   };
   Item cur = item_at(0);
+  // the next item's fields, read one item ahead (the slot below a bin's last
+  // item still lies inside its plan block: header and page words precede it)
+  Item nxt = item_at(1);
   int wcur = words[0];
   int wnext = words[1];
   const int n_items = bp[0], n_pages = bp[1];
@@ -480,27 +483,39 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     return x;
   };
 
-  // lane (dim column n, group g) holds heads 4g..4g+3 of dims 16b + n.
-  auto write_out = [&](int sq, const f32x4* oo, float ll) __attribute__((always_inline)) {
+  // A whole sequence's output: normalised at the item's end into this
+  // wave's LDS output rows (lane (dim column n, group g) holds heads
+  // 4g..4g+3 of dims 16b + n), then stored from there in 16-byte pieces
+  // (the G heads of KV head h are contiguous in out) at the start of the
+  // next step, before that step's page loads: stores issued after a page's
+  // loads would make the single wait at the top of the loop, which serves
+  // every path, also wait for them; issued before them, they complete within
+  // the wait for the page.
+  unsigned char* ol = smem + hgw * (TL::BYTES + SG::BYTES) + wave * (G * D * (int)sizeof(T));
+  auto finish_out = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * g + i;
-      const float li = from_lane(ll, i);  // lane r holds head r's sum
+      const float li = from_lane(l_run, i);  // lane r holds head r's sum
       if (r < G) {
         const float inv = 1.f / li;   // one division per row, not per element
 #pragma unroll
         for (int b = 0; b < NDB; ++b)
-          out[((int64_t)sq * Hq + h * G + r) * D + 16 * b + n] = (T)(oo[b][i] * inv);
+          *reinterpret_cast<T*>(ol + (r * D + 16 * b + n) * (int)sizeof(T)) = (T)(o[b][i] * inv);
       }
     }
   };
-  // A whole sequence's output, held until the next step has copied its page
-  // and writes it before sending that step's page loads: stores issued after
-  // a page's loads would make the single wait at the top of the loop, which
-  // serves every path, also wait for them (a store round trip per item);
-  // issued before them, they complete within the wait for the page.
-  f32x4 wo_o[NDB];
-  float wo_l = 1.f;
+  auto write_out = [&](int sq) __attribute__((always_inline)) {
+    constexpr int NCK = G * D * (int)sizeof(T) / 16;
+    T* dst = out + ((int64_t)sq * Hq + h * G) * D;
+#pragma unroll
+    for (int c0 = 0; c0 < NCK; c0 += 64) {
+      const int c = c0 + lane;
+      if (c < NCK)
+        *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(dst) + c * 16) =
+            *reinterpret_cast<const u32x4*>(ol + c * 16);
+    }
+  };
   int wo_seq = -1;   // -1: nothing held
 
   // The current item's last page: write the new row (fused append) and patch
@@ -569,9 +584,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   auto end_item = [&](int p) __attribute__((always_inline)) {
     if (cur.slot < 0) {
       wo_seq = cur.seq;
-      wo_l = l_run;
-#pragma unroll
-      for (int b = 0; b < NDB; ++b) wo_o[b] = o[b];
+      finish_out();
     } else {
       flush_arrival();   // at most one deferred arrival at a time
       const bool last = cur.flags & kItemLast;
@@ -619,7 +632,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
         stage_load(it_idx, sq, fl, sgd);
         stage_store(sgd);
       }
-      cur = item_at(it_idx);
+      cur = nxt;
+      nxt = item_at(it_idx + 1);
       take_item(it_idx);
       it_start = it_end;
       it_end += cur.np;
@@ -695,15 +709,15 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       *reinterpret_cast<vec8*>(vl + loff) = vr[k];
     }
     wave_lds_sync();
+    if (wo_seq >= 0) {      // the previous item's output, before this step's loads
+      write_out(wo_seq);
+      wo_seq = -1;
+    }
     if (p == it_start && (cur.flags & kItemLast) && cur.slot >= 0 && lane == 0)
       b_count = __hip_atomic_load(counters + (int64_t)cur.seq * n_kv_heads + h,
                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wcur = wnext;
     wnext = words[p + 2];   // inside the plan block: its words are followed by items
-    if (wo_seq >= 0) {      // the previous item's output, before this step's loads
-      write_out(wo_seq, wo_o, wo_l);
-      wo_seq = -1;
-    }
     load_page(p + 1, wcur, kr, vr);
     compute(p);
     PKV_TL(if (p == 0) tl_first = __builtin_amdgcn_s_memrealtime();)
@@ -720,7 +734,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     wave_lds_sync();  // this page's tile reads are done before the next copy
   }
   PKV_TL(const unsigned long long tl_last = __builtin_amdgcn_s_memrealtime();)
-  if (wo_seq >= 0) write_out(wo_seq, wo_o, wo_l);
+  if (wo_seq >= 0) write_out(wo_seq);
   flush_arrival();
 #ifdef PKV_TIMELINE
   {
@@ -741,7 +755,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
 
 template <typename T, int D, int G>
 static size_t decode_lds_bytes(int hgw) {
-  return (size_t)hgw * (Tile<T, D>::BYTES + Stage<T, D, G>::BYTES);
+  return (size_t)hgw * (Tile<T, D>::BYTES + Stage<T, D, G>::BYTES + G * D * sizeof(T));
 }
 
 template <typename T, int D, int G>
