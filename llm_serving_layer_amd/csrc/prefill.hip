@@ -150,6 +150,9 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
   // earlier, so the count cannot prove a tile landed if the two mix.)
   const int npages = (kv_len + PS - 1) / PS;
   const uint32_t rowbytes = (uint32_t)(row * sizeof(T));
+  // ids at or past this are out of range (kv_indices entries are int32)
+  const uint32_t nb32 = num_blocks > 0x7fffffffLL ? 0x80000000u : (uint32_t)num_blocks;
+  static_assert(TT % PS == 0, "a tile starts at a page boundary");
   auto page_of = [&](int t, int k) { return (t * TT + ((k * 4 + wave) * 64) / CPR) / PS; };
   auto load_ids = [&](int t, int* ids) {   // this wave's page ids for tile t
 #pragma unroll
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
       const int row0 = c0 / CPR;
       const int pg = page_of(t, k);
       const int raw = ids[k];
-      const bool bad = raw < 0 || (int64_t)raw >= num_blocks;
+      const bool bad = (uint32_t)raw >= nb32;   // (negative ids too)
       if (bad && pg < npages && lane == 0) flag(status, PKV_STATUS_BAD_PAGE);
       const int live_rows = bad ? 0 : min(PS, kv_len - pg * PS);   // <= 0 past the end
       const int64_t pid = bad ? 0 : raw;
@@ -176,8 +179,8 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
           ws_rsrc(const_cast<T*>(vpool) + pid * PS * row, range);
       const int rr = row0 + lane / CPR;              // the lane's row of the tile
       const int lc = (((lane % CPR) ^ xr(rr)) & 7) | ((lane % CPR) & ~7);  // its chunk
-      const uint32_t off = (uint32_t)((t * TT + rr) % PS) * rowbytes +
-                           (uint32_t)(h * RB + lc * 16);
+      // (a tile starts at a page boundary: the row within its page is rr % PS)
+      const uint32_t off = (uint32_t)(rr % PS) * rowbytes + (uint32_t)(h * RB + lc * 16);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rk, (__attribute__((address_space(3))) void*)(dst + c0 * 16), 16, off, 0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -263,17 +266,9 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
     // The previous tile's PV (zero probabilities before the first tile), its
     // matrix instructions interleaved with the softmax's vector ones below.
     pv_mma(va);
-    // Raw-score row max (scale_log2 > 0, so scaling commutes with max).
-    float mx = -INFINITY;
-#pragma unroll
-    for (int hf = 0; hf < NH; ++hf) {
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, s[hf][rr]);
-    }
-    mx = max_x32(mx) * scale_log2;
-    // Probabilities against the running reference m_run, taken while the
-    // tile's max is still being reduced: 16-key block (hf, qq) of P^T uses
-    // the lane's scores rr = 8 qq .. 8 qq + 7 in that order.
+    // Probabilities against the running reference m_run: 16-key block
+    // (hf, qq) of P^T uses the lane's scores rr = 8 qq .. 8 qq + 7 in that
+    // order.
     float ls = 0.f;
     auto probs = [&]() {
       ls = 0.f;
@@ -301,12 +296,23 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // then vector work
     }
-    // Lazy rescale: the reference max only moves when a row's max grows by
-    // more than 2^8 (then p <= 256, exact in the pool dtype's range); the
-    // result o / l does not depend on which reference is used. When it
-    // moves (always on the first tile), o (with the previous tile's PV
+    // Lazy rescale: the reference only moves when some lane's sum of its
+    // probabilities passes 2^12, which bounds every one of them by 2^12
+    // (within the pool dtype's range; NaN or inf counts as past it, as on the
+    // first tile, whose reference is -inf); the result o / l does not depend
+    // on which reference is used. Only then is the row max taken: it is at
+    // least 8 above the reference (a sum past 2^12 over 16 keys has a term
+    // past 2^8), so the reference grows, o (with the previous tile's PV
     // added) and l are rescaled and the probabilities taken again.
-    if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f)) {
+    if (__builtin_amdgcn_ballot_w64(!(ls <= 4096.f))) {
+      // raw-score row max (scale_log2 > 0, so scaling commutes with max)
+      float mx = -INFINITY;
+#pragma unroll
+      for (int hf = 0; hf < NH; ++hf) {
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, s[hf][rr]);
+      }
+      mx = max_x32(mx) * scale_log2;
       const float m_new = fmaxf(m_run, mx);   // finite: key 0 is visible to every row
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
