@@ -266,6 +266,59 @@ def test_matrix_core_prefill_matches_generic_kernel(dtype):
     assert diff <= (4e-3 if dtype == torch.float16 else 3.2e-2), diff
 
 
+@pytest.mark.parametrize("profile", ["rising", "falling", "alternating"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_running_reference_under_score_profiles(profile, dtype):
+    """The matrix-core prefill keeps each row's softmax reference until some
+    lane's sum of its probabilities passes 2^12 (then every probability it
+    holds is at most 2^12), and only then takes the row max and rescales.
+    Scores built to move the reference on every 32-key tile (rising by
+    about 11 in log2 units a tile), never after the first (falling), or on
+    every other tile (alternating), over a 600-token history and a
+    300-token chunk, against the oracle."""
+    print(f"prefill running reference: {profile} scores, {dtype}", flush=True)
+    n_kv, n_heads, d = 8, 32, 64
+    p = Pair(1, 256, 16, n_kv, n_heads, d, dtype=dtype)
+    assert p.gpu.q_tile == 128 // (n_heads // n_kv), "matrix-core prefill expected"
+    alloc, _keep = fragmented_allocator(256, 16)
+    seqs = [SequenceBlocks(alloc, seq_id=i) for i in range(2)]
+    g = torch.Generator().manual_seed(31)
+    u = torch.ones(d) / d ** 0.5
+
+    def kv_rows(first, n):
+        t = torch.arange(first, first + n, dtype=torch.float32)
+        if profile == "rising":
+            f = t / 32.0
+        elif profile == "falling":
+            f = (1000.0 - t) / 32.0
+        else:
+            f = torch.where((t // 32) % 2 == 0, t / 32.0, torch.zeros_like(t))
+        # every KV head's key row along u, scaled by f(position), plus noise
+        k = f[:, None, None] * u + 0.05 * torch.randn(n, n_kv, d, generator=g)
+        v = torch.randn(n, n_kv, d, generator=g)
+        return k.to(dtype), v.to(dtype)
+
+    tol, rtol = (2e-3, 1e-2) if dtype == torch.float16 else (1.6e-2, 8e-2)
+    for counts, first in (([600, 40], 0), ([300, 1], 600)):
+        meta = grow_and_assemble(seqs, counts, 16)
+        meta_gpu = _to_dev(meta)
+        T = meta.n_tokens
+        ks, vs = [], []
+        for i, n in enumerate(counts):
+            k, v = kv_rows(first if i == 0 else first // 15, n)
+            ks.append(k)
+            vs.append(v)
+        k, v = torch.cat(ks), torch.cat(vs)
+        # query rows along u: scores 64 * f(key) / 8, in log2 units x 0.18
+        q = (64.0 * u + 0.05 * torch.randn(T, n_heads, d, generator=g)).to(dtype)
+        p.gpu.append_kv(0, k.to(DEV), v.to(DEV), meta_gpu)
+        out = p.gpu.attend(q.to(DEV), 0, 0.125, meta_gpu)
+        p.ref.append_kv(0, k.float(), v.float(), meta)
+        want = p.ref.attend(q.float(), 0, 0.125, meta)
+        check([(0, out, want)], f"{profile} first={first}", tol, rtol)
+    p.gpu.check_device_errors()
+
+
 def test_prefill_with_a_negative_scale_matches_the_oracle():
     """The matrix-core prefill takes the row max before scaling, so it
     declines a non-positive scale; the generic kernel then serves the same
