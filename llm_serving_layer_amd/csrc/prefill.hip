@@ -9,26 +9,28 @@
 // triu(diagonal = kv_len - q_len + 1) mask) and sees keys 0..position.
 //
 // The KV axis is walked 32 tokens (two pages) at a time. A tile of K and of
-// V (those rows x head_dim of head h) is loaded two tiles ahead into
-// registers, staged in one of two padded LDS buffers, and read by every
+// V (those rows x head_dim of head h) goes straight from memory into one of
+// four LDS buffers (a ring; direct-to-LDS buffer loads two tiles ahead,
+// rows unpadded with their 16-byte chunks swizzled) and is read by every
 // wave. All products are 32x32x16 MFMAs, so every LDS byte read feeds 32
 // query rows:
 //  * S^T = K Q^T: K rows from LDS as the A operand, Q^T held in registers
 //    as the B operand. Lane (row n, group g) gets 16 scores of its query row
 //    n: keys 8 i + 4 g + 0..3, i = 0..3;
-//  * online softmax per query row, lane-local but for one half swap
-//    (v_permlane32_swap) per max / sum;
+//  * online softmax per query row, lane-local; the two half-waves holding a
+//    row meet (v_permlane32_swap) only for a row max and for the final sum;
 //  * O^T = V^T P^T: V^T from transposing LDS reads as the A operand, the
 //    lane's own 8 probabilities of a 16-key block as the B operand (the
 //    contraction index runs over keys 4 g + 0..3, 8 + 4 g + 0..3 of the
 //    block). Every O^T accumulator of a lane belongs to its own query row,
 //    so rescaling needs no cross-lane traffic.
-// The running max moves lazily: only when a row's max grows by more than
-// 2^8 (in exp2 units) are the accumulators rescaled, so probabilities stay
-// at most 256 and o / l is unchanged. Tiles wholly below the causal
-// diagonal skip the mask. Each wave's share of a tile lies within one page,
-// so page ids are scalar reads and pages are buffer ranges: rows past
-// kv_len read zeros without a memory access.
+// The running reference moves lazily: probabilities are taken against it,
+// and only when some lane's sum of a tile's probabilities passes 2^12 is
+// the row max taken and the accumulators rescaled, so probabilities stay at
+// most 2^12 and o / l is unchanged. Tiles wholly below the causal diagonal
+// skip the mask. Each wave's share of a tile lies within one page, so page
+// ids are scalar reads and pages are buffer ranges: rows past kv_len read
+// zeros without a memory access.
 // Numerics as serving/backends/paged_torch.py:443-485: scores, softmax and
 // accumulation in fp32; probabilities rounded to the pool dtype before PV.
 // The scale must be positive (the row max is taken before scaling); other
