@@ -42,6 +42,22 @@ def test_library_exports_every_declared_symbol():
     assert lib.pkv_abi_version() == _native.ABI_VERSION
 
 
+def test_integration_stub_matches_the_binding_table():
+    """The ctypes stub the integration guide gives a maintainer to copy binds
+    the same functions with the same argument lists as the package, and
+    checks the library's current ABI version."""
+    text = (HEADER.parents[1] / "INTEGRATION.md").read_text()
+    stub = text[text.index("SIG = {"):text.index("\n}", text.index("SIG = {"))]
+    entries = re.findall(r'"(pkv_\w+)":\s*\(C\.(\w+),\s*\[([^\]]*)\]', stub)
+    assert {name for name, _, _ in entries} == set(_native.SIGNATURES)
+    kinds = {"P": C.c_void_p, "I32": C.c_int32, "I64": C.c_int64, "F32": C.c_float}
+    for name, res, args in entries:
+        assert getattr(C, res) is _native.SIGNATURES[name][0], name
+        got = [kinds[a.strip()] for a in args.split(",") if a.strip()]
+        assert got == list(_native.SIGNATURES[name][1]), name
+    assert f"pkv_abi_version() == {_native.ABI_VERSION}" in text
+
+
 def _role(it):
     """0: a cut sequence's piece before its last, 1: a whole sequence,
     2: a cut sequence's last piece (it merges)."""
