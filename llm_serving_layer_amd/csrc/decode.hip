@@ -16,9 +16,11 @@
 //    about the same number of pages. A bin is one workgroup per group of up
 //    to 4 KV heads, and the grid is only as large as what stays resident, so
 //    no workgroup waits for a slot and all of them stream until about the
-//    same time. In a bin, the pieces of cut sequences come first, so their
-//    merges happen while other workgroups are still streaming; whole
-//    sequences come last.
+//    same time. In a bin, the pieces of cut sequences that are not their
+//    sequence's last come first (they publish while everything streams),
+//    whole sequences next, and last pieces at the end (a last piece reads
+//    its sequence's arrival count when it starts and, if every other piece
+//    has published, merges at its end without publishing its own).
 //  * Waves. Each wave owns one KV head and runs the bin's page stream on its
 //    own (no workgroup barrier anywhere): it loads its head's 128-byte slice
 //    of every token row (whole cache lines, eight lanes a row) into registers
