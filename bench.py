@@ -558,7 +558,8 @@ def bench_argmax(args):
 
 def bench_timeline(args):
     """
-    Ramp / steady / tail of one headline decode launch, from the per-wave
+    Ramp / steady / tail of one decode launch (the headline step, or with
+    --timeline-of capacity-a the capacity workload's phase A), from the per-wave
     records of the instrumented build (100 MHz s_memrealtime ticks): each wave
     (one KV head of one bin) records its start, the end of its first and last
     page, its end (after any merge), its page and item counts, and its merges
@@ -576,7 +577,15 @@ def bench_timeline(args):
                            "PKV_LIBRARY=llm_serving_layer_amd/_native/libpagedkv_timeline.so")
     lib.pkv_timeline_read.restype = C.c_int
     lib.pkv_timeline_read.argtypes = [C.c_void_p, C.c_int64]
-    lens = lognormal_lengths(256, 256)
+    if args.timeline_of == "capacity-a":
+        # the capacity workload's phase A: 4096 sequences of uniform[16, 64]
+        # tokens (the same lengths as bench_capacity), on a pool twice their pages
+        rng = random.Random(SEED)
+        lens = [rng.randint(16, 64) for _ in range(4096)]
+        what = "capacity phase A (4096 sequences, uniform[16,64] tokens)"
+    else:
+        lens = lognormal_lengths(256, 256)
+        what = "batch-256 headline step (lognormal mean 258)"
     pages = sum(-(-n // BS) for n in lens)
     bk, meta, step, _, ctx = decode_setup("cuda:0", lens, 2 * pages, args.part_pages)
     log("graph replay (instrumented build)")
@@ -607,9 +616,8 @@ def bench_timeline(args):
     line = base_line(
         args, "decode launch timeline (per-wave, instrumented build)", round(span, 2), "us",
         graph["ms_per_step"], "fp16",
-        ("one paged decode launch of the batch-256 headline step (lognormal mean 258), "
-         f"{GEOM}"),
-        batch=256, pages=pages, part_pages=args.part_pages)
+        f"one paged decode launch of the {what}, {GEOM}",
+        batch=len(lens), pages=pages, part_pages=args.part_pages)
     # record w: wave w % waves of workgroup w // waves = bin * groups + KV
     # head group, its dispatch index (round-robin over the 8 XCDs)
     hgw = 4 if HKV % 4 == 0 else 2 if HKV % 2 == 0 else 1
@@ -961,6 +969,8 @@ def main() -> int:
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "prefill", "copy", "swap", "capacity", "calib",
                              "timeline", "argmax"])
+    ap.add_argument("--timeline-of", default="headline", choices=["headline", "capacity-a"],
+                    help="timeline: the launch to record (the headline step or capacity phase A)")
     ap.add_argument("--part-pages", type=int, default=None,
                     help="split-K partition size in pages (default: the backend's)")
     ap.add_argument("--eager", action="store_true",
