@@ -261,6 +261,17 @@ template <typename T, int D, int G> struct Stage {
   static constexpr int BYTES = C * SLOT;
 };
 
+// A wave's ring of finished whole-sequence outputs in LDS: KO rows of the G
+// query heads of its KV head (OB bytes each) and their sequence ids, as many
+// as a wave's share of 80 KiB leaves beside its tile and item slots (so two
+// workgroups of four waves still fit a compute unit), at most 16.
+template <typename T, int D, int G> struct OutRing {
+  static constexpr int OB = G * D * (int)sizeof(T);
+  static constexpr int FREE = 20480 - Tile<T, D>::BYTES - Stage<T, D, G>::BYTES - 64;
+  static constexpr int KO = FREE / OB < 1 ? 1 : FREE / OB > 16 ? 16 : FREE / OB;
+  static constexpr int BYTES = KO * OB + 64;
+};
+
 // One workgroup per (bin, group of KV heads); wave w streams KV head
 // hg * waves + w through the bin's pages, one piece (item) after another,
 // without restarting the page pipeline at item boundaries. The bin's plan
@@ -485,16 +496,23 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     return x;
   };
 
-  // A whole sequence's output: normalised at the item's end into this
-  // wave's LDS output rows (lane (dim column n, group g) holds heads
-  // 4g..4g+3 of dims 16b + n), then stored from there in 16-byte pieces
-  // (the G heads of KV head h are contiguous in out) at the start of the
-  // next step, before that step's page loads: stores issued after a page's
-  // loads would make the single wait at the top of the loop, which serves
-  // every path, also wait for them; issued before them, they complete within
-  // the wait for the page.
-  unsigned char* ol = smem + hgw * (TL::BYTES + SG::BYTES) + wave * (G * D * (int)sizeof(T));
+  // A whole sequence's output: normalised at the item's end into the next
+  // row of this wave's LDS output ring (lane (dim column n, group g) holds
+  // heads 4g..4g+3 of dims 16b + n). The ring is stored in 16-byte pieces
+  // (the G heads of KV head h are contiguous in out) when it is full, at
+  // the start of the next step, before that step's page loads, and what it
+  // holds at the end of the stream: a bin of many short sequences writes its
+  // outputs in a few bursts instead of one store round among the page reads
+  // at every item (capacity phase A, 16 sequences a bin: 71.7 against 75.5
+  // us a launch). Stores issued after a page's loads would make the single
+  // wait at the top of the loop, which serves every path, also wait for
+  // them; issued before them, they complete within the wait for the page.
+  typedef OutRing<T, D, G> ORG;
+  unsigned char* ring = smem + hgw * (TL::BYTES + SG::BYTES) + wave * ORG::BYTES;
+  int32_t* ring_seq = reinterpret_cast<int32_t*>(ring + ORG::KO * ORG::OB);
+  int n_out = 0;   // outputs the ring holds
   auto finish_out = [&]() __attribute__((always_inline)) {
+    unsigned char* ol = ring + n_out * ORG::OB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * g + i;
@@ -507,18 +525,23 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       }
     }
   };
-  auto write_out = [&](int sq) __attribute__((always_inline)) {
-    constexpr int NCK = G * D * (int)sizeof(T) / 16;
-    T* dst = out + ((int64_t)sq * Hq + h * G) * D;
-#pragma unroll
-    for (int c0 = 0; c0 < NCK; c0 += 64) {
+  // The ring's first `cnt` rows to out: 16-byte piece c is piece c % NCK of
+  // row c / NCK. (A rolled loop: unrolled, its loads stay live and cost
+  // 30 VGPRs.)
+  auto write_out = [&](int cnt) __attribute__((always_inline)) {
+    constexpr int NCK = ORG::OB / 16;
+#pragma unroll 1
+    for (int c0 = 0; c0 < cnt * NCK; c0 += 64) {
       const int c = c0 + lane;
-      if (c < NCK)
-        *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(dst) + c * 16) =
-            *reinterpret_cast<const u32x4*>(ol + c * 16);
+      if (c < cnt * NCK) {
+        const int row = c / NCK;
+        T* dst = out + ((int64_t)ring_seq[row] * Hq + h * G) * D;
+        *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(dst) + (c - row * NCK) * 16) =
+            *reinterpret_cast<const u32x4*>(ring + c * 16);
+      }
     }
   };
-  int wo_seq = -1;   // -1: nothing held
+  bool ring_full = false;
 
   // The current item's last page: write the new row (fused append) and patch
   // the loaded copy when slot_mapping agrees with the page table.
@@ -585,8 +608,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   // Item end: the output (whole sequence), or the partial of a cut sequence.
   auto end_item = [&](int p) __attribute__((always_inline)) {
     if (cur.slot < 0) {
-      wo_seq = cur.seq;
       finish_out();
+      if (lane == 0) ring_seq[n_out] = cur.seq;
+      ring_full = ++n_out == ORG::KO;
     } else {
       flush_arrival();   // at most one deferred arrival at a time
       const bool last = cur.flags & kItemLast;
@@ -711,9 +735,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       *reinterpret_cast<vec8*>(vl + loff) = vr[k];
     }
     wave_lds_sync();
-    if (wo_seq >= 0) {      // the previous item's output, before this step's loads
-      write_out(wo_seq);
-      wo_seq = -1;
+    if (ring_full) {      // the ring's outputs, before this step's loads
+      write_out(ORG::KO);
+      ring_full = false;
+      n_out = 0;
     }
     if (p == it_start && (cur.flags & kItemLast) && cur.slot >= 0 && lane == 0)
       b_count = __hip_atomic_load(counters + (int64_t)cur.seq * n_kv_heads + h,
@@ -736,7 +761,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     wave_lds_sync();  // this page's tile reads are done before the next copy
   }
   PKV_TL(const unsigned long long tl_last = __builtin_amdgcn_s_memrealtime();)
-  if (wo_seq >= 0) write_out(wo_seq);
+  if (n_out > 0) {
+    wave_lds_sync();   // the last output's rows and sequence id
+    write_out(n_out);
+  }
   flush_arrival();
 #ifdef PKV_TIMELINE
   {
@@ -757,7 +785,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
 
 template <typename T, int D, int G>
 static size_t decode_lds_bytes(int hgw) {
-  return (size_t)hgw * (Tile<T, D>::BYTES + Stage<T, D, G>::BYTES + G * D * sizeof(T));
+  return (size_t)hgw * (Tile<T, D>::BYTES + Stage<T, D, G>::BYTES + OutRing<T, D, G>::BYTES);
 }
 
 template <typename T, int D, int G>
