@@ -261,15 +261,26 @@ template <typename T, int D, int G> struct Stage {
   static constexpr int BYTES = C * SLOT;
 };
 
-// A wave's ring of finished whole-sequence outputs in LDS: KO rows of the G
-// query heads of its KV head (OB bytes each) and their sequence ids, as many
-// as a wave's share of 80 KiB leaves beside its tile and item slots (so two
-// workgroups of four waves still fit a compute unit), at most 16.
-template <typename T, int D, int G> struct OutRing {
+// A wave's two rings in LDS, for the stores it defers: KR new K/V row
+// slices of its KV head (the fused append; RB2 bytes each) with their
+// slots, and KO finished whole-sequence outputs (the rows of the G query
+// heads of its KV head; OB bytes each) with their sequence ids. They share
+// what a wave's share of 80 KiB leaves beside its tile and item slots (so
+// two workgroups of four waves still fit a compute unit): the row ring up
+// to half of it, the output ring the rest, each at most 16 entries. At
+// head_dim 128 there is no row ring (KR = 0: the new rows are stored at
+// once): its code would take the one-query-head kernel past 256 VGPRs, to
+// one wave a SIMD.
+template <typename T, int D, int G> struct Rings {
   static constexpr int OB = G * D * (int)sizeof(T);
-  static constexpr int FREE = 20480 - Tile<T, D>::BYTES - Stage<T, D, G>::BYTES - 64;
-  static constexpr int KO = FREE / OB < 1 ? 1 : FREE / OB > 16 ? 16 : FREE / OB;
-  static constexpr int BYTES = KO * OB + 64;
+  static constexpr int RB2 = 2 * D * (int)sizeof(T);
+  static constexpr int FREE = 20480 - Tile<T, D>::BYTES - Stage<T, D, G>::BYTES - 2 * 64;
+  static constexpr int KR0 = (FREE / 2 < FREE - OB ? FREE / 2 : FREE - OB) / RB2;
+  static constexpr int KR = D > 64 ? 0 : KR0 < 1 ? 1 : KR0 > 16 ? 16 : KR0;
+  static constexpr int KO0 = (FREE - KR * RB2) / OB;
+  static constexpr int KO = KO0 < 1 ? 1 : KO0 > 16 ? 16 : KO0;
+  static constexpr int ROWS = KR * RB2 + 64;     // row slices, then 16 slot ids
+  static constexpr int BYTES = ROWS + KO * OB + 64;
 };
 
 // One workgroup per (bin, group of KV heads); wave w streams KV head
@@ -496,23 +507,48 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     return x;
   };
 
-  // A whole sequence's output: normalised at the item's end into the next
-  // row of this wave's LDS output ring (lane (dim column n, group g) holds
-  // heads 4g..4g+3 of dims 16b + n). The ring is stored in 16-byte pieces
-  // (the G heads of KV head h are contiguous in out) when it is full, at
-  // the start of the next step, before that step's page loads, and what it
-  // holds at the end of the stream: a bin of many short sequences writes its
-  // outputs in a few bursts instead of one store round among the page reads
-  // at every item (capacity phase A, 16 sequences a bin: 71.7 against 75.5
-  // us a launch). Stores issued after a page's loads would make the single
-  // wait at the top of the loop, which serves every path, also wait for
-  // them; issued before them, they complete within the wait for the page.
-  typedef OutRing<T, D, G> ORG;
-  unsigned char* ring = smem + hgw * (TL::BYTES + SG::BYTES) + wave * ORG::BYTES;
-  int32_t* ring_seq = reinterpret_cast<int32_t*>(ring + ORG::KO * ORG::OB);
-  int n_out = 0;   // outputs the ring holds
+  // Deferred stores. A whole sequence's output is normalised at the item's
+  // end into the next entry of this wave's LDS output ring (lane (dim column
+  // n, group g) holds heads 4g..4g+3 of dims 16b + n), and the fused
+  // append's new row slices go to the row ring instead of the pool. A full
+  // ring is stored in 16-byte pieces at the start of the next step, before
+  // that step's page loads, and whatever the rings hold at the end of the
+  // stream: a bin of many short sequences then writes in a few bursts
+  // instead of a round of stores among the page reads at every item
+  // (capacity phase A, 16 sequences a bin: 67.5 against 75.5 us a launch).
+  // No other wave of the launch reads a new row's slot (the fusion's
+  // precondition), and the kernel patches its own loaded copy at once, so
+  // the deferral changes no result. Stores issued after a page's loads
+  // would make the single wait at the top of the loop, which serves every
+  // path, also wait for them; issued before them, they complete within the
+  // wait for the page.
+  typedef Rings<T, D, G> RG;
+  unsigned char* rrow = smem + hgw * (TL::BYTES + SG::BYTES) + wave * RG::BYTES;
+  int32_t* rrow_slot = reinterpret_cast<int32_t*>(rrow + RG::KR * RG::RB2);
+  unsigned char* ring = rrow + RG::ROWS;
+  int32_t* ring_seq = reinterpret_cast<int32_t*>(ring + RG::KO * RG::OB);
+  int n_out = 0;    // outputs the output ring holds
+  int n_rows = 0;   // row slices the row ring holds
+  bool rows_full = false;
+  // The row ring's first `cnt` entries to the pools: 16-byte piece c is
+  // piece c % NCR of entry c / NCR (K slice, then V slice).
+  auto write_rows = [&](int cnt) __attribute__((always_inline)) {
+    constexpr int NCR = RG::RB2 / 16;
+    constexpr int HALF = NCR / 2;
+#pragma unroll 1
+    for (int c0 = 0; c0 < cnt * NCR; c0 += 64) {
+      const int c = c0 + lane;
+      if (c < cnt * NCR) {
+        const int e = c / NCR, part = c - e * NCR;
+        unsigned char* d = reinterpret_cast<unsigned char*>(
+            (part < HALF ? kpool : vpool) + (int64_t)rrow_slot[e] * row_elems);
+        *reinterpret_cast<u32x4*>(d + h * RB + (part % HALF) * 16) =
+            *reinterpret_cast<const u32x4*>(rrow + c * 16);
+      }
+    }
+  };
   auto finish_out = [&]() __attribute__((always_inline)) {
-    unsigned char* ol = ring + n_out * ORG::OB;
+    unsigned char* ol = ring + n_out * RG::OB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * g + i;
@@ -529,7 +565,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   // row c / NCK. (A rolled loop: unrolled, its loads stay live and cost
   // 30 VGPRs.)
   auto write_out = [&](int cnt) __attribute__((always_inline)) {
-    constexpr int NCK = ORG::OB / 16;
+    constexpr int NCK = RG::OB / 16;
 #pragma unroll 1
     for (int c0 = 0; c0 < cnt * NCK; c0 += 64) {
       const int c = c0 + lane;
@@ -554,16 +590,33 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       return;
     }
     const bool patch = (int64_t)new_slot == page * PS + tl;
-    unsigned char* kd = reinterpret_cast<unsigned char*>(kpool + new_slot * row_elems);
-    unsigned char* vd = reinterpret_cast<unsigned char*>(vpool + new_slot * row_elems);
+    if constexpr (RG::KR > 0) {   // into the row ring's next entry
+      unsigned char* e = rrow + n_rows * RG::RB2;
+      if (lane == 0) rrow_slot[n_rows] = new_slot;
+      rows_full = ++n_rows == RG::KR;
 #pragma unroll
-    for (int k = 0; k < NLD; ++k) {
-      if (k * RPI + lrow0 == tl) {
-        *reinterpret_cast<vec8*>(kd + h * RB + lcol) = kx;
-        *reinterpret_cast<vec8*>(vd + h * RB + lcol) = vx;
-        if (patch) {
-          kq[k] = kx;
-          vq[k] = vx;
+      for (int k = 0; k < NLD; ++k) {
+        if (k * RPI + lrow0 == tl) {
+          *reinterpret_cast<vec8*>(e + lcol) = kx;
+          *reinterpret_cast<vec8*>(e + RB + lcol) = vx;
+          if (patch) {
+            kq[k] = kx;
+            vq[k] = vx;
+          }
+        }
+      }
+    } else {                      // into the pools at once
+      unsigned char* kd = reinterpret_cast<unsigned char*>(kpool + new_slot * row_elems);
+      unsigned char* vd = reinterpret_cast<unsigned char*>(vpool + new_slot * row_elems);
+#pragma unroll
+      for (int k = 0; k < NLD; ++k) {
+        if (k * RPI + lrow0 == tl) {
+          *reinterpret_cast<vec8*>(kd + h * RB + lcol) = kx;
+          *reinterpret_cast<vec8*>(vd + h * RB + lcol) = vx;
+          if (patch) {
+            kq[k] = kx;
+            vq[k] = vx;
+          }
         }
       }
     }
@@ -610,7 +663,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     if (cur.slot < 0) {
       finish_out();
       if (lane == 0) ring_seq[n_out] = cur.seq;
-      ring_full = ++n_out == ORG::KO;
+      ring_full = ++n_out == RG::KO;
     } else {
       flush_arrival();   // at most one deferred arrival at a time
       const bool last = cur.flags & kItemLast;
@@ -735,8 +788,13 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       *reinterpret_cast<vec8*>(vl + loff) = vr[k];
     }
     wave_lds_sync();
-    if (ring_full) {      // the ring's outputs, before this step's loads
-      write_out(ORG::KO);
+    if (RG::KR > 0 && rows_full) {   // full rings, before this step's loads
+      write_rows(RG::KR);
+      rows_full = false;
+      n_rows = 0;
+    }
+    if (ring_full) {
+      write_out(RG::KO);
       ring_full = false;
       n_out = 0;
     }
@@ -761,10 +819,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
     wave_lds_sync();  // this page's tile reads are done before the next copy
   }
   PKV_TL(const unsigned long long tl_last = __builtin_amdgcn_s_memrealtime();)
-  if (n_out > 0) {
-    wave_lds_sync();   // the last output's rows and sequence id
-    write_out(n_out);
-  }
+  if (n_rows + n_out > 0) wave_lds_sync();   // the last entries and their ids
+  if (RG::KR > 0 && n_rows > 0) write_rows(n_rows);
+  if (n_out > 0) write_out(n_out);
   flush_arrival();
 #ifdef PKV_TIMELINE
   {
@@ -785,7 +842,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
 
 template <typename T, int D, int G>
 static size_t decode_lds_bytes(int hgw) {
-  return (size_t)hgw * (Tile<T, D>::BYTES + Stage<T, D, G>::BYTES + OutRing<T, D, G>::BYTES);
+  return (size_t)hgw * (Tile<T, D>::BYTES + Stage<T, D, G>::BYTES + Rings<T, D, G>::BYTES);
 }
 
 template <typename T, int D, int G>
