@@ -6,9 +6,9 @@
 // One workgroup (16 waves) per row. Threads stride over the row in 16-byte
 // chunks, sixteen chunks in flight (256 KiB per workgroup: a whole 128 256
 // fp16 row in one round trip; eight for bf16), each keeping its best (value,
-// index); the
-// 1024 candidates meet in a wave shuffle tree and then across the 16 waves.
-// HBM-bound: a row of V logits is read once.
+// index); the 1024 candidates meet in a wave shuffle tree and then across the
+// 16 waves. HBM-bound: a row of V logits is read once, so the loads carry the
+// streaming hint (nt) and leave the caches to other data.
 #include "mfma.h"
 
 namespace pkv {
@@ -142,7 +142,8 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const T* __restr
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t c = c0 + (int64_t)u * NT + tid;
-      w[u] = c < nchunk ? *reinterpret_cast<const u32x4*>(x + c * V) : u32x4{0u, 0u, 0u, 0u};
+      w[u] = c < nchunk ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + c * V))
+                        : u32x4{0u, 0u, 0u, 0u};
     }
     float rb = -INFINITY;
     int rc = -1;                        // the round's first chunk with the largest number
