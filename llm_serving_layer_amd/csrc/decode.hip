@@ -448,7 +448,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
                     (w < SG::QC + SG::RC ? k_new : v_new) + (int64_t)si * row_elems + h * D) +
                 (w < SG::QC + SG::RC ? w - SG::QC : w - SG::QC - SG::RC) * 16;
       }
-      d[r] = src ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
+      // each read once per item: streaming hint
+      d[r] = src ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src))
+                 : u32x4{0u, 0u, 0u, 0u};
     }
   };
   auto stage_store = [&](const u32x4* d) __attribute__((always_inline)) {
