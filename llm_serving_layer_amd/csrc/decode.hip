@@ -533,7 +533,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
   int n_rows = 0;   // row slices the row ring holds
   bool rows_full = false;
   // The row ring's first `cnt` entries to the pools: 16-byte piece c is
-  // piece c % NCR of entry c / NCR (K slice, then V slice).
+  // piece c % NCR of entry c / NCR (K slice, then V slice). Both rings are
+  // written with the streaming hint: nothing in this launch reads them back.
   auto write_rows = [&](int cnt) __attribute__((always_inline)) {
     constexpr int NCR = RG::RB2 / 16;
     constexpr int HALF = NCR / 2;
@@ -544,8 +545,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
         const int e = c / NCR, part = c - e * NCR;
         unsigned char* d = reinterpret_cast<unsigned char*>(
             (part < HALF ? kpool : vpool) + (int64_t)rrow_slot[e] * row_elems);
-        *reinterpret_cast<u32x4*>(d + h * RB + (part % HALF) * 16) =
-            *reinterpret_cast<const u32x4*>(rrow + c * 16);
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(rrow + c * 16),
+                                    reinterpret_cast<u32x4*>(d + h * RB + (part % HALF) * 16));
       }
     }
   };
@@ -574,8 +575,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_kernel(
       if (c < cnt * NCK) {
         const int row = c / NCK;
         T* dst = out + ((int64_t)ring_seq[row] * Hq + h * G) * D;
-        *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(dst) + (c - row * NCK) * 16) =
-            *reinterpret_cast<const u32x4*>(ring + c * 16);
+        __builtin_nontemporal_store(
+            *reinterpret_cast<const u32x4*>(ring + c * 16),
+            reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(dst) + (c - row * NCK) * 16));
       }
     }
   };
